@@ -1,0 +1,303 @@
+"""Monarch-Muon optimizer-step benchmark on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload 6.89b-nb4] [--no-cpu-baseline]
+
+Runs the full ``MonarchMuonOptimizer.step()`` (Muon group: momentum, bf16
+Newton-Schulz over every Monarch block, apply; AdamW group) of the named
+workload on synthetic data already resident in HBM, times exactly K steps
+between two device synchronisations, and prints one JSON line.  The dominant
+kernel's roofline comes from per-launch hipEvents on the launch stream over
+extra instrumented steps; the CPU baseline times the oracle (the CPU
+restatement of the reference step) on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import statistics
+import sys
+import time
+from collections import defaultdict
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "optimizer-step ms, 6.89B-ref nb=4 bf16; NS TFLOP/s as % of bf16 MFMA peak"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+REFERENCE_H100_MS = 304.4   # README.md:16 (bf16 momentum, H100)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- workload
+def build_gpu(w, device, seed=0):
+    from monarch_muon_amd import CoatStateMonarchMuon, MonarchMuonOptimizer, QuantizationConfig, _abi
+    from monarch_muon_amd.workloads import parameter_inventory
+    gen = torch.Generator(device=device).manual_seed(seed)
+    muon, adamw, bufs = [], [], []
+    for _, shape, is_muon in parameter_inventory(w):
+        p = (torch.randn(shape, generator=gen, device=device) * 0.02).to(w.param_dtype).requires_grad_(True)
+        p.grad = (torch.randn(shape, generator=gen, device=device) * 1e-3).to(w.param_dtype)
+        (muon if is_muon else adamw).append(p)
+        if is_muon and w.prefill_momentum:
+            bufs.append(torch.randn(shape, generator=gen, device=device) * 1e-3)
+    if w.momentum_dtype == "fp8":
+        opt = CoatStateMonarchMuon(muon, adamw, lr=0.02, momentum=0.95, qargs=QuantizationConfig(),
+                                   ns_dtype=w.ns_dtype)
+        for p, b in zip(muon, bufs):
+            st = opt.state[p]
+            groups = (b.numel() + 127) // 128
+            codes = torch.empty(b.shape, dtype=torch.float8_e4m3fn, device=device)
+            meta = [torch.empty(groups, dtype=torch.float32, device=device) for _ in range(3)]
+            _abi.fp8_quantize(b.contiguous(), codes.view(torch.uint8), *meta, signed=True)
+            st["momentum_buffer"] = codes
+            for key, t in zip(("scale", "expand", "sqrt_minmax"), meta):
+                st[f"{key}_momentum_buffer"] = t
+    else:
+        opt = MonarchMuonOptimizer(muon, adamw, lr=0.02, momentum=0.95, ns_dtype=w.ns_dtype)
+        for p, b in zip(muon, bufs):
+            opt.state[p]["momentum_buffer"] = b.to(w.momentum_dtype)
+    del bufs
+    torch.cuda.synchronize()
+    return muon, adamw, opt
+
+
+# ---------------------------------------------------------------- per-kernel timing
+def instrumented_step(opt, lr=0.02):
+    """One optimizer step with a hipEvent pair around every launch (on the
+    stream the kernels run on).  Returns [(kernel, group, seconds_event_pair)]."""
+    from monarch_muon_amd import _abi
+    from monarch_muon_amd.optim import _COEFFS
+    from monarch_muon_amd.plan import NS_STEPS
+    lib = _abi.lib()
+    out = []
+    muon_group, adam_group = opt.param_groups
+    fp8 = type(opt).__name__ == "CoatStateMonarchMuon"
+    for gl in opt._muon_planner.groups:
+        stream = _abi.stream_handle(gl.key[0])
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        if fp8:
+            _abi.check(lib.mmuon_fp8_momentum_pack(C.byref(gl.struct), 0.95, 1, stream), "pack")
+        else:
+            _abi.check(lib.mmuon_momentum_pack(C.byref(gl.struct), 0.95, stream), "pack")
+        e1.record()
+        out.append(("pack", gl, 0, e0, e1))
+        for it in range(NS_STEPS):
+            for st in range(3):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                _abi.check(lib.mmuon_ns_stage(C.byref(gl.struct), it, NS_STEPS, st, _COEFFS,
+                                              -lr * gl.alpha_scale, 0, stream), "ns_stage")
+                e1.record()
+                out.append((("syrk", "poly", "px")[st], gl, it, e0, e1))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    opt._adamw_step(adam_group, lr)
+    e1.record()
+    out.append(("adamw", None, 0, e0, e1))
+    torch.cuda.synchronize()
+    return [(k, gl, it, e0.elapsed_time(e1)) for k, gl, it, e0, e1 in out]
+
+
+def kernel_symbol(kind, gl, it):
+    """The device-function family rocprof reports for a launch."""
+    if kind == "syrk":
+        return "ns_sym_bf16<0>"
+    if kind == "poly":
+        return "ns_sym_bf16<1>"
+    if kind == "px":
+        if it < 4:
+            return "ns_px_bf16<2,true>"
+        return "ns_px_bf16<3,false>" if gl.transposed else "ns_px_bf16<3,true>"
+    if kind == "pack":
+        return "pack_cols" if gl.transposed else "pack_rows"
+    return kind
+
+
+def stage_flops(kind, gl):
+    """Algorithmic FLOPs of one launch (full products, symmetry not credited)."""
+    lay = gl.ws.layout
+    m, n, N = lay.m, lay.n, gl.nblocks
+    if kind == "syrk":
+        return 2.0 * m * m * n * N
+    if kind == "poly":
+        return 2.0 * m * m * m * N
+    if kind == "px":
+        return 2.0 * m * m * n * N
+    return 0.0
+
+
+def stage_exec_flops(kind, gl):
+    """MFMA FLOPs the kernels execute (padded tiles; symmetric stages compute the
+    upper-triangle tiles only)."""
+    lay = gl.ws.layout
+    N, mp, np_ = gl.nblocks, lay.mp, lay.np_
+    nt = mp // 256
+    sym = nt * (nt + 1) / 2 / (nt * nt)
+    kx = -(-lay.n // 64) * 64
+    if kind == "syrk":
+        return 2.0 * mp * mp * kx * N * sym
+    if kind == "poly":
+        return 2.0 * mp * mp * mp * N * sym
+    if kind == "px":
+        return 2.0 * mp * mp * np_ * N
+    return 0.0
+
+
+def pack_bytes(gl, momentum_bytes, grad_bytes=2, x_bytes=2):
+    lay = gl.ws.layout
+    return gl.nblocks * lay.m * lay.n * (grad_bytes + 2 * momentum_bytes + x_bytes)
+
+
+# ---------------------------------------------------------------- CPU baseline
+def cpu_baseline(w, seed=0):
+    """The oracle step on the host cores over a bounded sample: the Muon blocks
+    of one transformer layer plus 1/n_layer of the AdamW elements; scaled by
+    n_layer to one full step."""
+    from oracle.step import ReferenceMonarchMuon
+    from monarch_muon_amd.workloads import parameter_inventory
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(seed)
+    muon, adamw, bufs = [], [], []
+    for name, shape, is_muon in parameter_inventory(w):
+        if ".h." in name and int(name.split(".")[2]) != 0:
+            continue
+        if not is_muon and len(shape) == 2:
+            shape = (max(1, shape[0] // w.n_layer), shape[1])
+        p = (torch.randn(shape, generator=gen) * 0.02).to(w.param_dtype).requires_grad_(True)
+        p.grad = (torch.randn(shape, generator=gen) * 1e-3).to(w.param_dtype)
+        (muon if is_muon else adamw).append(p)
+        if is_muon:
+            bufs.append(torch.randn(shape, generator=gen) * 1e-3)
+    variant = "membench" if w.ns_dtype == torch.bfloat16 else "pretrain"
+    opt = ReferenceMonarchMuon(muon, adamw, lr=0.02, momentum=0.95, variant=variant)
+    for p, b in zip(muon, bufs):
+        opt.state[p]["momentum_buffer"] = b if w.momentum_dtype == "fp8" else b.to(w.momentum_dtype)
+    opt.step()  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        opt.step()
+        times.append(time.perf_counter() - t0)
+    sample_ms = statistics.median(times) * 1e3
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": round(sample_ms * w.n_layer, 1), "unit": "ms", "cores": threads, "kind": "port",
+            "sample": f"oracle step (torch CPU) over layer 0's Muon blocks + 1/{w.n_layer} of the AdamW "
+                      f"elements, median of 3 after 1 warm-up = {sample_ms:.1f} ms, x{w.n_layer} layers",
+            "cpu_model": model, "os_cpu_count": os.cpu_count()}
+
+
+# ---------------------------------------------------------------- main
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=12)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="6.89b-nb4")
+    ap.add_argument("--instrumented", type=int, default=2, help="extra per-kernel-timed steps")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures the single-GPU optimizer step only; multi-GPU runs are not part of "
+              "this build (see DESIGN.md for how the step would shard).", file=sys.stderr)
+        sys.exit(2)
+    from monarch_muon_amd.workloads import WORKLOADS, adamw_elements, muon_elements, ns_flops
+    w = WORKLOADS[args.workload]
+    dev = torch.device("cuda", 0)
+    log(f"[bench] building workload {w.name} on {torch.cuda.get_device_name(dev)}")
+    muon, adamw, opt = build_gpu(w, dev)
+    log(f"[bench] warm-up {args.warmup} steps")
+    for _ in range(args.warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    log(f"[bench] timing {args.steps} steps")
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s, e in evs:
+        s.record()
+        opt.step()
+        e.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    step_ms = [s.elapsed_time(e) for s, e in evs]
+    median_ms = statistics.median(step_ms)
+    log(f"[bench] {wall_ms:.2f} ms/step (wall), median event {median_ms:.2f} ms")
+
+    # per-kernel timing
+    per = defaultdict(lambda: [0.0, 0, 0.0, 0.0])   # symbol -> [ms, launches, alg flops, exec flops]
+    stage_ms = defaultdict(float)
+    for _ in range(max(1, args.instrumented)):
+        for kind, gl, it, ms in instrumented_step(opt):
+            sym = kernel_symbol(kind, gl, it)
+            rec = per[sym]
+            rec[0] += ms
+            rec[1] += 1
+            if gl is not None:
+                rec[2] += stage_flops(kind, gl)
+                rec[3] += stage_exec_flops(kind, gl)
+            stage_ms[kind] += ms
+    reps = max(1, args.instrumented)
+    ns_ms = sum(stage_ms[k] for k in ("syrk", "poly", "px")) / reps
+    ns_tf = ns_flops(w) / (ns_ms * 1e-3) / 1e12
+    dominant = max((k for k in per if k.startswith("ns_")), key=lambda k: per[k][0])
+    d_ms, d_n, d_fl, d_ex = per[dominant]
+    d_avg = d_ms / d_n
+    achieved = (d_fl / d_n) / (d_avg * 1e-3) / 1e12
+    kernels = {k: {"avg_ms": round(v[0] / v[1], 4), "launches_per_step": v[1] // reps,
+                   "ms_per_step": round(v[0] / reps, 3),
+                   **({"alg_tflops": round(v[2] / (v[0] * 1e-3) / 1e12, 1),
+                       "exec_tflops": round(v[3] / (v[0] * 1e-3) / 1e12, 1)} if v[2] else {})}
+               for k, v in sorted(per.items(), key=lambda kv: -kv[1][0])}
+    mom_bytes = 4 if w.momentum_dtype == torch.float32 else (2 if w.momentum_dtype == torch.bfloat16 else 1)
+    pack_ms = stage_ms["pack"] / reps
+    pack_b = sum(pack_bytes(gl, mom_bytes) for gl in opt._muon_planner.groups)
+    res = {
+        "metric": METRIC, "value": round(wall_ms, 3), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall_ms, 3), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,.02) weights, N(0,1e-3) grads and momentum, resident in HBM)",
+        "config": {"workload": w.name, "layers": w.n_layer, "hidden": w.n_embd, "intermediate": w.intermediate,
+                   "nblocks": w.nblocks, "muon_elements": muon_elements(w), "adamw_elements": adamw_elements(w),
+                   "param_dtype": str(w.param_dtype).split(".")[-1],
+                   "momentum_dtype": w.momentum_dtype if isinstance(w.momentum_dtype, str)
+                   else str(w.momentum_dtype).split(".")[-1],
+                   "newton_schulz": "bf16 MFMA, fp32 accumulate, 5 iterations",
+                   "groups": [f"{gl.rows}x{gl.cols}x{gl.nblocks}" for gl in opt._muon_planner.groups]},
+        "median_event_ms": round(median_ms, 3),
+        "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "avg_launch_ms": round(d_avg, 4),
+                     "alg_flops_per_launch": d_fl / d_n, "exec_tflops": round((d_ex / d_n) / (d_avg * 1e-3) / 1e12, 1)},
+        "newton_schulz": {"ms": round(ns_ms, 3), "alg_tflop": round(ns_flops(w) / 1e12, 2),
+                          "alg_tflops": round(ns_tf, 1), "frac_peak": round(ns_tf / PEAK_BF16_TFLOPS, 4)},
+        "momentum_pack": {"ms": round(pack_ms, 3), "alg_bytes": pack_b,
+                          "gbs": round(pack_b / (pack_ms * 1e-3) / 1e9, 1),
+                          "frac_hbm": round(pack_b / (pack_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+        "adamw_ms": round(stage_ms["adamw"] / reps, 3),
+        "kernels": kernels,
+        "reference_h100_ms": REFERENCE_H100_MS,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (oracle on host cores, bounded sample)")
+        res["cpu_baseline"] = cpu_baseline(w)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

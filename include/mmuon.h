@@ -1,0 +1,199 @@
+/*
+ * mmuon.h -- C ABI of libmmuon.so, the MI355X (gfx950) implementation of the
+ * Monarch-Muon optimizer step.
+ *
+ * The reference has no native boundary on this path: its step is a sequence
+ * of torch ops (membench/src/models/monarch/monarch_muon.py:140-208,
+ * pretrain/src/models/monarch/monarch_muon.py:139-201,
+ * pretrain/src/models/monarch/coat_state_muon.py:22-139).  Each entry point
+ * below names the reference lines whose work it replaces.
+ *
+ * Conventions
+ *  - All pointers inside descriptors are DEVICE addresses owned by the caller
+ *    (torch allocates every tensor, table and workspace); the library keeps
+ *    no device allocations and no state between calls.
+ *  - Every launch is enqueued on the caller's stream; no call synchronises.
+ *  - Return value 0 = success; a negative MMUON_E* code otherwise, with a
+ *    message retrievable through mmuon_last_error() (thread-local).
+ *  - Descriptors are read on the host during the call only.
+ */
+#ifndef MMUON_H
+#define MMUON_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types */
+enum {
+  MMUON_F32 = 0,
+  MMUON_BF16 = 1,
+  MMUON_F8E4M3 = 2 /* OCP float8_e4m3fn payload, with per-128 fp32 metadata */
+};
+
+/* error codes */
+enum {
+  MMUON_OK = 0,
+  MMUON_EINVAL = -1,   /* bad argument (shape, dtype, null pointer, alignment) */
+  MMUON_EHIP = -2,     /* a HIP runtime call failed */
+  MMUON_ERANGE = -3    /* size beyond what a kernel's indexing supports */
+};
+
+/* One Monarch block (one r x c slice of a (nb, r, c) factor). */
+typedef struct mmuon_block_ref {
+  void* param;       /* r*c elements, row-major, param dtype      */
+  const void* grad;  /* r*c elements, grad dtype                  */
+  void* buf;         /* r*c elements, momentum dtype (F32/BF16), or the
+                        e4m3 payload for the FP8-state path            */
+} mmuon_block_ref;
+
+/* FP8 metadata of one block: per 128-element group of the block's slice of the
+   flattened parameter (the groups never straddle blocks; see
+   mmuon_fp8_momentum_pack). */
+typedef struct mmuon_block_fp8 {
+  float* scale;
+  float* expand;
+  float* sqrt_minmax;
+} mmuon_block_fp8;
+
+/* Workspace geometry of one same-shape group, from mmuon_ns_layout(). */
+typedef struct mmuon_ns_layout_t {
+  int32_t m, n;        /* Newton-Schulz orientation: m = min(r,c), n = max(r,c) */
+  int32_t mp, np_;     /* padded m, n (multiples of the kernels' tiles)          */
+  int32_t nparts;      /* partial sums of squares per block                      */
+  int32_t ns_dtype;    /* MMUON_BF16 or MMUON_F32                                */
+  int64_t x_bytes;     /* one X stack  [N][mp][np_]                               */
+  int64_t a_bytes;     /* one Gram stack [N][mp][mp]                              */
+  int64_t part_bytes;  /* partial sums   [N][nparts] fp32                         */
+} mmuon_ns_layout_t;
+
+/* A same-shape group of blocks, in the reference's grouping order. */
+#define MMUON_GROUP_ALIGNED16 1  /* every block pointer is 16-byte aligned */
+typedef struct mmuon_group {
+  int32_t rows, cols;            /* block shape as stored (r, c)                 */
+  int32_t nblocks;               /* N                                            */
+  int32_t param_dtype;           /* F32 / BF16                                   */
+  int32_t grad_dtype;            /* F32 / BF16                                   */
+  int32_t buf_dtype;             /* F32 / BF16 / F8E4M3                          */
+  int32_t ns_dtype;              /* BF16 (membench copy) or F32 (pretrain copy)  */
+  int32_t flags;                 /* MMUON_GROUP_* bits                           */
+  const mmuon_block_ref* blocks; /* device table, N entries                      */
+  const mmuon_block_fp8* fp8;    /* device table, N entries (FP8 path), or NULL  */
+  void* x0;                      /* workspace: X stack  (layout.x_bytes)         */
+  void* x1;                      /* workspace: X stack  (layout.x_bytes)         */
+  void* a;                       /* workspace: Gram     (layout.a_bytes)         */
+  void* p;                       /* workspace: polynomial (layout.a_bytes)       */
+  float* partial;                /* workspace: layout.part_bytes                 */
+  float* scale;                  /* workspace: N floats                          */
+} mmuon_group;
+
+/* Geometry and workspace sizes for a group of (rows x cols) blocks.
+   Replaces nothing in the reference (the reference allocates implicitly in
+   torch.cat / bmm: membench monarch_muon.py:161-164). */
+int mmuon_ns_layout(int32_t rows, int32_t cols, int32_t ns_dtype, int64_t nblocks,
+                    mmuon_ns_layout_t* out);
+
+/* Heavy-ball momentum + stack + cast, in one pass over the group:
+     buf <- momentum*buf + grad          (rounded to the buffer dtype per op)
+     X   <- cast(buf) to ns_dtype, transposed when rows > cols, into g->x0
+     scale[b] <- 1 / (||X_b||_F + 1e-7), the Frobenius normalisation factor
+   Replaces membench monarch_muon.py:146-151 (_foreach_mul_/_foreach_add_),
+   :161-163 (torch.cat + .to(bf16)), :38 (the norm's reduction) and :40-41
+   (the transpose); pretrain monarch_muon.py:143-148,158. */
+int mmuon_momentum_pack(const mmuon_group* g, float momentum, void* stream);
+
+/* FP8-state variant of mmuon_momentum_pack: buf holds e4m3 codes with the
+   per-128 metadata of g->fp8; dequantize -> momentum -> stack/cast -> requantize.
+   `have_state` = 0 treats the momentum as zeros (first step, where the reference
+   creates it with zeros_like).  Requires rows*cols % 128 == 0.
+   Replaces coat_state_muon.py:126-139 (dequantize/quantize_ around the step,
+   :94-114) fused with the work of mmuon_momentum_pack. */
+int mmuon_fp8_momentum_pack(const mmuon_group* g, float momentum, int32_t have_state,
+                            void* stream);
+
+/* Newton-Schulz over the group's stack (already packed into g->x0) followed by
+   the weight update:
+     X <- X / (||X||_F + 1e-7)  (norm from the packed partial sums)
+     repeat iters: A = X X^T ; P = b A + c A A ; X = a X + P X
+     param <- param + alpha * cast(X) (un-transposed), alpha = -lr*sqrt(r/c)
+   coeffs = {a, b, c}.  flags: MMUON_NS_NO_APPLY leaves the final X in the
+   workspace (x0 when iters is even, x1 otherwise) and does not touch params.
+   Replaces membench monarch_muon.py:36-50 (_newton_schulz_batched, with the
+   norm at :38-39), :164-170 (cast back, split, _foreach_add_ apply);
+   pretrain monarch_muon.py:36-50,159-165. */
+#define MMUON_NS_NO_APPLY 1
+int mmuon_newton_schulz_apply(const mmuon_group* g, int32_t iters, const float coeffs[3],
+                              float alpha, int32_t flags, void* stream);
+
+/* One stage of one Newton-Schulz iteration (stage 0 = Gram X X^T, 1 = polynomial,
+   2 = X update; on the last iteration stage 2 also applies the weight update
+   unless MMUON_NS_NO_APPLY).  mmuon_newton_schulz_apply is exactly the loop
+   over (iteration, stage); this entry exists so a caller can time each kernel
+   with its own events.  Same reference lines as mmuon_newton_schulz_apply. */
+int mmuon_ns_stage(const mmuon_group* g, int32_t iteration, int32_t iters, int32_t stage,
+                   const float coeffs[3], float alpha, int32_t flags, void* stream);
+
+/* Embedded AdamW over a list of tensors (one launch). */
+typedef struct mmuon_adamw_tensor {
+  void* param;        /* numel elements, param dtype */
+  const void* grad;   /* grad dtype                  */
+  void* exp_avg;      /* state dtype (or e4m3 codes) */
+  void* exp_avg_sq;   /* state dtype (or e4m3 codes) */
+  int64_t numel;
+} mmuon_adamw_tensor;
+
+typedef struct mmuon_adamw_args {
+  const mmuon_adamw_tensor* tensors; /* device table                                  */
+  const int64_t* chunks;             /* device: per chunk (tensor << 40 | first elem)  */
+  int64_t nchunks;
+  int32_t chunk_elems;               /* elements per chunk (128 on the FP8 path)       */
+  int32_t param_dtype, grad_dtype, state_dtype;
+  int32_t apply_weight_decay;        /* weight_decay > 0                               */
+  /* scalars as the reference forms them in double and hands to torch ops */
+  float wd_factor;                   /* 1 - lr * weight_decay                          */
+  float beta1, beta2;
+  float one_minus_beta1, one_minus_beta2;
+  float sqrt_bc2;                    /* sqrt(1 - beta2 ** step)                        */
+  float eps;
+  float neg_step_size;               /* -lr / (1 - beta1 ** step)                      */
+} mmuon_adamw_args;
+
+/* Replaces membench monarch_muon.py:176-208 (foreach AdamW: decoupled weight
+   decay, bias corrections, eps after sqrt(v)/sqrt(bc2)) and pretrain
+   :171-201.  state_dtype F32 or BF16. */
+int mmuon_adamw(const mmuon_adamw_args* a, void* stream);
+
+/* FP8-state AdamW: exp_avg (signed) and exp_avg_sq (unsigned) held as e4m3 with
+   per-128 metadata; chunk_elems must be 128 (one metadata group per chunk).
+   have_state = 0: the moments start from zero (first step).
+   Replaces coat_state_muon.py:128-138 around membench :176-208. */
+typedef struct mmuon_adamw_fp8_tensor {
+  float* scale_m; float* expand_m; float* sqrt_minmax_m;
+  float* scale_v; float* expand_v; float* sqrt_minmax_v;
+} mmuon_adamw_fp8_tensor;
+int mmuon_adamw_fp8(const mmuon_adamw_args* a, const mmuon_adamw_fp8_tensor* meta,
+                    int32_t have_state, void* stream);
+
+/* Stand-alone codec over one flat tensor (numel elements):
+   quantize: fp32 values -> e4m3 codes + scale/expand/sqrt_minmax per 128-group
+   dequantize: the inverse.  Replaces coat_state_muon.py:94-114 (_quantize_kernel
+   :46-91, _dequantize_kernel :22-43).  signed_ = 1 for first-order states. */
+int mmuon_fp8_quantize(const float* value, uint8_t* codes, float* scale, float* expand,
+                       float* sqrt_minmax, int64_t numel, int32_t signed_, void* stream);
+int mmuon_fp8_dequantize(const uint8_t* codes, const float* scale, const float* expand,
+                         const float* sqrt_minmax, float* out, int64_t numel,
+                         int32_t signed_, void* stream);
+
+/* Thread-local message of the last failing call ("" if none). */
+const char* mmuon_last_error(void);
+
+/* ABI version: bumped on any change to this header. */
+int mmuon_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MMUON_H */

@@ -1,0 +1,158 @@
+"""ctypes binding of ``libmmuon.so`` (the C ABI declared in ``include/mmuon.h``).
+
+The library is loaded lazily on first use and must exist: there is no
+fallback implementation, so a missing or unloadable library raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(os.environ.get("MMUON_LIB", Path(__file__).resolve().parent / "libmmuon.so"))
+
+F32, BF16, F8E4M3 = 0, 1, 2
+GROUP_ALIGNED16 = 1
+NS_NO_APPLY = 1
+ABI_VERSION = 1
+
+_DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8E4M3}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPES[dt]
+    except KeyError:
+        raise TypeError(f"libmmuon supports float32, bfloat16 and float8_e4m3fn tensors, not {dt}") from None
+
+
+class BlockRef(C.Structure):
+    _fields_ = [("param", C.c_void_p), ("grad", C.c_void_p), ("buf", C.c_void_p)]
+
+
+class BlockFp8(C.Structure):
+    _fields_ = [("scale", C.c_void_p), ("expand", C.c_void_p), ("sqrt_minmax", C.c_void_p)]
+
+
+class NsLayout(C.Structure):
+    _fields_ = [("m", C.c_int32), ("n", C.c_int32), ("mp", C.c_int32), ("np_", C.c_int32),
+                ("nparts", C.c_int32), ("ns_dtype", C.c_int32),
+                ("x_bytes", C.c_int64), ("a_bytes", C.c_int64), ("part_bytes", C.c_int64)]
+
+
+class Group(C.Structure):
+    _fields_ = [("rows", C.c_int32), ("cols", C.c_int32), ("nblocks", C.c_int32),
+                ("param_dtype", C.c_int32), ("grad_dtype", C.c_int32), ("buf_dtype", C.c_int32),
+                ("ns_dtype", C.c_int32), ("flags", C.c_int32),
+                ("blocks", C.c_void_p), ("fp8", C.c_void_p),
+                ("x0", C.c_void_p), ("x1", C.c_void_p), ("a", C.c_void_p), ("p", C.c_void_p),
+                ("partial", C.c_void_p), ("scale", C.c_void_p)]
+
+
+class AdamWTensor(C.Structure):
+    _fields_ = [("param", C.c_void_p), ("grad", C.c_void_p), ("exp_avg", C.c_void_p),
+                ("exp_avg_sq", C.c_void_p), ("numel", C.c_int64)]
+
+
+class AdamWArgs(C.Structure):
+    _fields_ = [("tensors", C.c_void_p), ("chunks", C.c_void_p), ("nchunks", C.c_int64),
+                ("chunk_elems", C.c_int32), ("param_dtype", C.c_int32), ("grad_dtype", C.c_int32),
+                ("state_dtype", C.c_int32), ("apply_weight_decay", C.c_int32),
+                ("wd_factor", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float),
+                ("one_minus_beta1", C.c_float), ("one_minus_beta2", C.c_float),
+                ("sqrt_bc2", C.c_float), ("eps", C.c_float), ("neg_step_size", C.c_float)]
+
+
+class AdamWFp8Tensor(C.Structure):
+    _fields_ = [("scale_m", C.c_void_p), ("expand_m", C.c_void_p), ("sqrt_minmax_m", C.c_void_p),
+                ("scale_v", C.c_void_p), ("expand_v", C.c_void_p), ("sqrt_minmax_v", C.c_void_p)]
+
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "mmuon_abi_version": (C.c_int, []),
+    "mmuon_last_error": (C.c_char_p, []),
+    "mmuon_ns_layout": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int64, C.POINTER(NsLayout)]),
+    "mmuon_momentum_pack": (C.c_int, [C.POINTER(Group), C.c_float, C.c_void_p]),
+    "mmuon_fp8_momentum_pack": (C.c_int, [C.POINTER(Group), C.c_float, C.c_int32, C.c_void_p]),
+    "mmuon_newton_schulz_apply": (C.c_int, [C.POINTER(Group), C.c_int32, C.POINTER(C.c_float),
+                                            C.c_float, C.c_int32, C.c_void_p]),
+    "mmuon_ns_stage": (C.c_int, [C.POINTER(Group), C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_float),
+                                 C.c_float, C.c_int32, C.c_void_p]),
+    "mmuon_adamw": (C.c_int, [C.POINTER(AdamWArgs), C.c_void_p]),
+    "mmuon_adamw_fp8": (C.c_int, [C.POINTER(AdamWArgs), C.POINTER(AdamWFp8Tensor), C.c_int32,
+                                  C.c_void_p]),
+    "mmuon_fp8_quantize": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                     C.c_int64, C.c_int32, C.c_void_p]),
+    "mmuon_fp8_dequantize": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.c_int64, C.c_int32, C.c_void_p]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Load ``libmmuon.so`` once; raise if it is missing or has another ABI."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m monarch_muon_amd.build` "
+                "(the MI355X kernels have no fallback)")
+        handle = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        if handle.mmuon_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI {handle.mmuon_abi_version()}, expected {ABI_VERSION}")
+        _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().mmuon_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ns_layout(rows: int, cols: int, ns_dtype: int, nblocks: int) -> NsLayout:
+    out = NsLayout()
+    check(lib().mmuon_ns_layout(rows, cols, ns_dtype, nblocks, C.byref(out)), "mmuon_ns_layout")
+    return out
+
+
+def fp8_quantize(value: torch.Tensor, codes: torch.Tensor, scale: torch.Tensor, expand: torch.Tensor,
+                 sqrt_minmax: torch.Tensor, signed: bool) -> None:
+    """Stand-alone codec: fp32 ``value`` -> e4m3 ``codes`` + per-128 metadata (in place)."""
+    _require_cuda(value, codes, scale, expand, sqrt_minmax)
+    assert value.dtype == torch.float32 and value.is_contiguous()
+    assert codes.dtype in (torch.uint8, torch.float8_e4m3fn) and codes.is_contiguous()
+    groups = (value.numel() + 127) // 128
+    for t in (scale, expand, sqrt_minmax):
+        assert t.dtype == torch.float32 and t.numel() >= groups and t.is_contiguous()
+    check(lib().mmuon_fp8_quantize(value.data_ptr(), codes.data_ptr(), scale.data_ptr(), expand.data_ptr(),
+                                   sqrt_minmax.data_ptr(), value.numel(), int(signed),
+                                   stream_handle(value.device)), "mmuon_fp8_quantize")
+
+
+def fp8_dequantize(codes: torch.Tensor, scale: torch.Tensor, expand: torch.Tensor,
+                   sqrt_minmax: torch.Tensor, out: torch.Tensor, signed: bool) -> None:
+    _require_cuda(codes, scale, expand, sqrt_minmax, out)
+    assert out.dtype == torch.float32 and out.is_contiguous() and codes.is_contiguous()
+    assert out.numel() == codes.numel()
+    check(lib().mmuon_fp8_dequantize(codes.data_ptr(), scale.data_ptr(), expand.data_ptr(),
+                                     sqrt_minmax.data_ptr(), out.data_ptr(), out.numel(), int(signed),
+                                     stream_handle(out.device)), "mmuon_fp8_dequantize")
+
+
+def _require_cuda(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if not t.is_cuda:
+            raise RuntimeError("libmmuon kernels need tensors on a ROCm GPU (no CPU path)")

@@ -1,0 +1,141 @@
+// Embedded AdamW of the Monarch-Muon optimizer as one multi-tensor launch.
+//
+// Per element, in the reference's op order (membench monarch_muon.py:196-208):
+//   p  <- R_p(p * (1 - lr wd))                         (when wd > 0)
+//   m  <- R_s(m * b1) ; m <- R_s(m + (1-b1) g)         (foreach add with alpha: fused)
+//   v  <- R_s(v * b2) ; v <- R_s(v + ((1-b2) g) g)     (addcmul)
+//   d  <- R_s(sqrt v) ; d <- R_s(d / sqrt(bc2)) ; d <- R_s(d + eps)
+//   p  <- R_p(p + (-lr/bc1) (m / d))                   (addcdiv)
+// R_x rounds to the tensor's dtype.  Algorithmic HBM traffic, bf16 p/g/m/v:
+// 14 B per element.
+#include "common.hpp"
+#include "fp8codec.hpp"
+#include "kernels.hpp"
+
+namespace mmuon {
+
+template <class TP, class TS>
+__device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v, const AdamWArgs& a) {
+  if (a.apply_wd) p = TP::round(p * a.wd_factor);
+  m = TS::round(m * a.beta1);
+  m = TS::round(fmaf(g, a.one_minus_beta1, m));
+  v = TS::round(v * a.beta2);
+  v = TS::round(v + (a.one_minus_beta2 * g) * g);
+  float d = TS::round(sqrtf(v));
+  d = TS::round(d / a.sqrt_bc2);
+  d = TS::round(d + a.eps);
+  p = TP::round(p + a.neg_step_size * (m / d));
+}
+
+constexpr int ADAM_NT = 256;
+
+template <class TP, class TG, class TS>
+__global__ __launch_bounds__(ADAM_NT) void adamw_kernel(AdamWArgs a) {
+  const int64_t code = a.chunks[blockIdx.x];
+  const int t = int(code >> 40);
+  const int64_t start = code & ((int64_t(1) << 40) - 1);
+  const mmuon_adamw_tensor T = a.tensors[t];
+  const int64_t end = min(T.numel, start + int64_t(a.chunk_elems));
+  auto* p = reinterpret_cast<typename TP::storage*>(T.param);
+  const auto* g = reinterpret_cast<const typename TG::storage*>(T.grad);
+  auto* m = reinterpret_cast<typename TS::storage*>(T.exp_avg);
+  auto* v = reinterpret_cast<typename TS::storage*>(T.exp_avg_sq);
+  for (int64_t i = start + threadIdx.x; i < end; i += ADAM_NT) {
+    float pv = TP::load(p, i), mv = TS::load(m, i), vv = TS::load(v, i);
+    adamw_elem<TP, TS>(pv, TG::load(g, i), mv, vv, a);
+    TP::store(p, i, pv);
+    TS::store(m, i, mv);
+    TS::store(v, i, vv);
+  }
+}
+
+int launch_adamw(const AdamWArgs& a, int param_dtype, int grad_dtype, int state_dtype,
+                 hipStream_t s) {
+  if (a.nchunks <= 0) return 0;
+  const dim3 grid(unsigned(a.nchunks)), block(ADAM_NT);
+#define MMUON_ADAM_CASE(PD, GD, SD, TP, TG, TS)                                  \
+  if (param_dtype == PD && grad_dtype == GD && state_dtype == SD) {              \
+    hipLaunchKernelGGL((adamw_kernel<TP, TG, TS>), grid, block, 0, s, a);        \
+    return 0;                                                                    \
+  }
+  MMUON_ADAM_CASE(MMUON_BF16, MMUON_BF16, MMUON_BF16, BF16T, BF16T, BF16T)
+  MMUON_ADAM_CASE(MMUON_BF16, MMUON_BF16, MMUON_F32, BF16T, BF16T, F32T)
+  MMUON_ADAM_CASE(MMUON_F32, MMUON_F32, MMUON_F32, F32T, F32T, F32T)
+  MMUON_ADAM_CASE(MMUON_F32, MMUON_F32, MMUON_BF16, F32T, F32T, BF16T)
+#undef MMUON_ADAM_CASE
+  return -1;
+}
+
+// ---------------------------------------------------------------------------
+// FP8-state AdamW: one wave per 128-element metadata group; the moments are
+// dequantized to fp32, updated in fp32 (the reference's dequantized states are
+// fp32 tensors), and requantized (exp_avg signed, exp_avg_sq unsigned).
+// chunk = tensor << 40 | first element of the group.
+// ---------------------------------------------------------------------------
+template <class TP, class TG>
+__global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
+  const int64_t gidx = int64_t(blockIdx.x) * (ADAM_NT / 64) + (threadIdx.x >> 6);
+  if (gidx >= a.nchunks) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t code = a.chunks[gidx];
+  const int t = int(code >> 40);
+  const int64_t start = code & ((int64_t(1) << 40) - 1);
+  const mmuon_adamw_tensor T = a.tensors[t];
+  const mmuon_adamw_fp8_tensor M = a.fp8[t];
+  const int64_t grp = start >> 7;
+  auto* p = reinterpret_cast<typename TP::storage*>(T.param);
+  const auto* g = reinterpret_cast<const typename TG::storage*>(T.grad);
+  uint8_t* qm = reinterpret_cast<uint8_t*>(T.exp_avg);
+  uint8_t* qv = reinterpret_cast<uint8_t*>(T.exp_avg_sq);
+  Fp8Meta mm{0.f, 0.f, 0.f}, mv{0.f, 0.f, 0.f};
+  if (a.have_state) {
+    mm = Fp8Meta{M.scale_m[grp], M.expand_m[grp], M.sqrt_minmax_m[grp]};
+    mv = Fp8Meta{M.scale_v[grp], M.expand_v[grp], M.sqrt_minmax_v[grp]};
+  }
+  float mo[2], vo[2];
+  bool ok[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int64_t i = start + lane + 64 * h;
+    ok[h] = i < T.numel;
+    mo[h] = vo[h] = 0.f;
+    if (ok[h]) {
+      float pv = TP::load(p, i);
+      float m = a.have_state ? fp8_dequant(qm[i], mm, true) : 0.f;
+      float v = a.have_state ? fp8_dequant(qv[i], mv, false) : 0.f;
+      adamw_elem<TP, F32T>(pv, TG::load(g, i), m, v, a);
+      TP::store(p, i, pv);
+      mo[h] = m;
+      vo[h] = v;
+    }
+  }
+  uint8_t c0, c1;
+  const Fp8Meta nm = fp8_quant_group(mo[0], mo[1], ok[0], ok[1], true, c0, c1);
+  if (ok[0]) qm[start + lane] = c0;
+  if (ok[1]) qm[start + lane + 64] = c1;
+  const Fp8Meta nv = fp8_quant_group(vo[0], vo[1], ok[0], ok[1], false, c0, c1);
+  if (ok[0]) qv[start + lane] = c0;
+  if (ok[1]) qv[start + lane + 64] = c1;
+  if (lane == 0) {
+    M.scale_m[grp] = nm.scale;
+    M.expand_m[grp] = nm.expand;
+    M.sqrt_minmax_m[grp] = nm.sqrt_minmax;
+    M.scale_v[grp] = nv.scale;
+    M.expand_v[grp] = nv.expand;
+    M.sqrt_minmax_v[grp] = nv.sqrt_minmax;
+  }
+}
+
+int launch_adamw_fp8(const AdamWArgs& a, int param_dtype, int grad_dtype, hipStream_t s) {
+  if (a.nchunks <= 0) return 0;
+  const dim3 grid(unsigned((a.nchunks + 3) / 4)), block(ADAM_NT);
+  if (param_dtype == MMUON_BF16 && grad_dtype == MMUON_BF16)
+    hipLaunchKernelGGL((adamw_fp8_kernel<BF16T, BF16T>), grid, block, 0, s, a);
+  else if (param_dtype == MMUON_F32 && grad_dtype == MMUON_F32)
+    hipLaunchKernelGGL((adamw_fp8_kernel<F32T, F32T>), grid, block, 0, s, a);
+  else
+    return -1;
+  return 0;
+}
+
+}  // namespace mmuon

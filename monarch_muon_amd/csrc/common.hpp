@@ -1,0 +1,81 @@
+// Shared device helpers for the gfx950 Monarch-Muon kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mmuon.h"
+
+namespace mmuon {
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32.  bf16 is carried as its raw 16-bit pattern; conversion is
+// round-to-nearest-even with quiet-NaN preservation (the rounding torch uses
+// for every bf16 tensor op).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+// round a float to bf16 precision and back
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// Element access by storage type tag.
+struct F32T {
+  using storage = float;
+  static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void store(float* p, int64_t i, float v) { p[i] = v; }
+  static __device__ __forceinline__ float round(float v) { return v; }
+};
+struct BF16T {
+  using storage = uint16_t;
+  static __device__ __forceinline__ float load(const uint16_t* p, int64_t i) { return bf2f(p[i]); }
+  static __device__ __forceinline__ void store(uint16_t* p, int64_t i, float v) { p[i] = f2bf(v); }
+  static __device__ __forceinline__ float round(float v) { return rbf(v); }
+};
+
+// ---------------------------------------------------------------------------
+// wave64 reductions (cross-lane through ds_swizzle/DPP as the compiler picks)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ int wave_isum(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// Block-wide sum for blockDim.x == NT (multiple of 64); result valid in thread 0.
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* scratch /* NT/64 floats */) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) scratch[wid] = v;
+  __syncthreads();
+  float r = 0.f;
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) r += scratch[w];
+  }
+  return r;
+}
+
+}  // namespace mmuon

@@ -1,0 +1,80 @@
+// Host-side launch interfaces shared between the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mmuon.h"
+
+namespace mmuon {
+
+struct PackArgs {
+  const mmuon_block_ref* blocks;
+  void* x;          // X stack [N][mp][np] in the NS dtype
+  float* partial;   // [N][nparts]
+  int N;
+  int m, n;         // NS orientation (m = min(rows, cols))
+  int mp, np;       // padded extents of the X stack
+  int nparts;
+  float mu;
+  int vec;          // 8-wide vector access is valid for every block
+};
+
+int pack_nparts(int mp, int np_, bool transposed);
+int launch_pack(const PackArgs& a, int grad_dtype, int buf_dtype, int x_dtype, bool transposed,
+                hipStream_t s);
+void launch_block_scale(const float* partial, int nparts, float* scale, int N, bool bf16_norm,
+                        hipStream_t s);
+
+// Newton-Schulz stage kernels -------------------------------------------------
+enum NsStage { NS_SYRK = 0, NS_POLY = 1, NS_PX = 2, NS_PX_APPLY = 3 };
+
+struct NsArgs {
+  const void* x_in;   // X stack [N][mp][np]
+  const void* a_in;   // Gram / polynomial stack [N][mp][mp]
+  void* out;          // stage output
+  const float* scale; // per-block 1/(||X||+eps) for the first iteration, else null
+  const mmuon_block_ref* blocks;  // apply stage: parameter pointers
+  int N, m, n, mp, np;
+  int kx;             // contraction extent of the Gram product (n rounded to the K tile)
+  float ca, cb, cc;   // quintic coefficients
+  float alpha;        // apply: -lr * sqrt(rows / cols)
+  int transposed;     // rows > cols
+};
+
+// geometry helpers (tile sizes of the kernels)
+int ns_tile_m(int ns_dtype);
+int ns_tile_n(int ns_dtype);
+int ns_tile_k(int ns_dtype);
+int launch_ns_stage(const NsArgs& a, int stage, int ns_dtype, int param_dtype, hipStream_t s);
+
+// AdamW ---------------------------------------------------------------------
+struct AdamWArgs {
+  const mmuon_adamw_tensor* tensors;
+  const int64_t* chunks;
+  int64_t nchunks;
+  int chunk_elems;
+  float wd_factor;      // 1 - lr * weight_decay
+  int apply_wd;         // weight_decay > 0
+  float beta1, one_minus_beta1, beta2, one_minus_beta2;
+  float sqrt_bc2;       // sqrt(1 - beta2^t)
+  float eps;
+  float neg_step_size;  // -lr / (1 - beta1^t)
+  const mmuon_adamw_fp8_tensor* fp8;
+  int have_state;
+};
+int launch_adamw(const AdamWArgs& a, int param_dtype, int grad_dtype, int state_dtype,
+                 hipStream_t s);
+int launch_adamw_fp8(const AdamWArgs& a, int param_dtype, int grad_dtype, hipStream_t s);
+
+// FP8 codec -------------------------------------------------------------------
+void launch_fp8_quantize(const float* v, uint8_t* q, float* sc, float* ex, float* smm,
+                         int64_t numel, bool sgn, hipStream_t s);
+void launch_fp8_dequantize(const uint8_t* q, const float* sc, const float* ex, const float* smm,
+                           float* out, int64_t numel, bool sgn, hipStream_t s);
+int fp8_pack_nparts(int rows, int cols, bool transposed);
+int launch_fp8_pack(const PackArgs& a, const mmuon_block_fp8* meta, int rows, int cols,
+                    int grad_dtype, int x_dtype, bool transposed, int have_state,
+                    hipStream_t s);
+
+}  // namespace mmuon

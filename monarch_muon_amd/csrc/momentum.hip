@@ -1,0 +1,234 @@
+// Fused heavy-ball momentum + stack + cast + per-block sum of squares.
+//
+// One pass over a same-shape group of Monarch blocks:
+//   buf <- round_B(round_B(buf * mu) + g)        (two torch ops, two roundings)
+//   X   <- round_X(buf)  in Newton-Schulz orientation (transposed if rows>cols)
+//   partial[b][wg] <- sum of X^2 over this workgroup's share of block b
+// Algorithmic HBM traffic per element (fp32 momentum, bf16 grad, bf16 X):
+// read g 2 B + read buf 4 B + write buf 4 B + write X 2 B = 12 B.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mmuon {
+
+template <class TB>
+__device__ __forceinline__ float momentum_update(float buf, float g, float mu) {
+  // compiled with -ffp-contract=off: the product is rounded before the sum,
+  // as torch's separate mul_ and add_ do.
+  const float t = TB::round(buf * mu);
+  return TB::round(t + g);
+}
+
+// 8 consecutive elements, vector access (16-B aligned for bf16, 32 B for fp32)
+template <class T>
+struct Vec8;
+template <>
+struct Vec8<BF16T> {
+  static __device__ __forceinline__ void load(const uint16_t* p, float v[8]) {
+    const uint4 r = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      v[2 * q] = __uint_as_float(w[q] << 16);
+      v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+    }
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const float v[8]) {
+    uint4 r;
+    r.x = uint32_t(f2bf(v[0])) | (uint32_t(f2bf(v[1])) << 16);
+    r.y = uint32_t(f2bf(v[2])) | (uint32_t(f2bf(v[3])) << 16);
+    r.z = uint32_t(f2bf(v[4])) | (uint32_t(f2bf(v[5])) << 16);
+    r.w = uint32_t(f2bf(v[6])) | (uint32_t(f2bf(v[7])) << 16);
+    *reinterpret_cast<uint4*>(p) = r;
+  }
+};
+template <>
+struct Vec8<F32T> {
+  static __device__ __forceinline__ void load(const float* p, float v[8]) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0];
+    const float4 b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  static __device__ __forceinline__ void store(float* p, const float v[8]) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+};
+
+constexpr int PACK_NT = 256;
+constexpr int PACK_ITERS = 4;
+constexpr int PACK_ELEMS = PACK_NT * 8 * PACK_ITERS;  // X elements per workgroup (row layout)
+constexpr int PACK_TILE = 64;                          // transposed layout: 64 x 64 tiles
+
+// rows <= cols: X[b][i][j] = buf[b][i][j]; the X stack is walked linearly.
+template <class TG, class TB, class TX>
+__global__ __launch_bounds__(PACK_NT) void pack_rows_kernel(PackArgs a) {
+  __shared__ float red[PACK_NT / 64];
+  const int b = blockIdx.y;
+  const mmuon_block_ref ref = a.blocks[b];
+  const auto* g = reinterpret_cast<const typename TG::storage*>(ref.grad);
+  auto* buf = reinterpret_cast<typename TB::storage*>(ref.buf);
+  auto* x = reinterpret_cast<typename TX::storage*>(a.x) + int64_t(b) * a.mp * a.np;
+  const int64_t total = int64_t(a.mp) * a.np;
+  float ss = 0.f;
+#pragma unroll
+  for (int it = 0; it < PACK_ITERS; ++it) {
+    const int64_t e = int64_t(blockIdx.x) * PACK_ELEMS + (int64_t(it) * PACK_NT + threadIdx.x) * 8;
+    if (e >= total) break;
+    const int i = int(e / a.np), j = int(e % a.np);
+    float v[8];
+    if (a.vec && i < a.m && j + 8 <= a.n) {
+      const int64_t s = int64_t(i) * a.n + j;
+      float gv[8], bv[8];
+      Vec8<TG>::load(g + s, gv);
+      Vec8<TB>::load(buf + s, bv);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) bv[q] = momentum_update<TB>(bv[q], gv[q], a.mu);
+      Vec8<TB>::store(buf + s, bv);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = TX::round(bv[q]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        v[q] = 0.f;
+        if (i < a.m && j + q < a.n) {
+          const int64_t s = int64_t(i) * a.n + j + q;
+          const float nb = momentum_update<TB>(TB::load(buf, s), TG::load(g, s), a.mu);
+          TB::store(buf, s, nb);
+          v[q] = TX::round(nb);
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) ss += v[q] * v[q];
+    Vec8<TX>::store(x + e, v);
+  }
+  const float tot = block_sum<PACK_NT>(ss, red);
+  if (threadIdx.x == 0) a.partial[int64_t(b) * a.nparts + blockIdx.x] = tot;
+}
+
+// rows > cols: X[b][i][j] = buf[b][j][i], transposed through a 64x64 LDS tile.
+template <class TG, class TB, class TX>
+__global__ __launch_bounds__(PACK_NT) void pack_cols_kernel(PackArgs a) {
+  __shared__ float tile[PACK_TILE][PACK_TILE + 1];
+  __shared__ float red[PACK_NT / 64];
+  const int b = blockIdx.y;
+  const int tiles_j = a.np / PACK_TILE;
+  const int ti = blockIdx.x / tiles_j, tj = blockIdx.x % tiles_j;
+  const int i0 = ti * PACK_TILE, j0 = tj * PACK_TILE;  // X coordinates
+  const mmuon_block_ref ref = a.blocks[b];
+  const auto* g = reinterpret_cast<const typename TG::storage*>(ref.grad);
+  auto* buf = reinterpret_cast<typename TB::storage*>(ref.buf);
+  auto* x = reinterpret_cast<typename TX::storage*>(a.x) + int64_t(b) * a.mp * a.np;
+  // phase 1: buf rows r = j0 + t/4, columns c = i0 + (t%4)*16 + [0,16)
+  {
+    const int jr = threadIdx.x >> 2, seg = (threadIdx.x & 3) * 16;
+    const int r = j0 + jr;  // buf row  (= X column)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = i0 + seg + h * 8;  // buf col (= X row)
+      float v[8];
+      if (a.vec && r < a.n && c + 8 <= a.m) {
+        const int64_t s = int64_t(r) * a.m + c;
+        float gv[8];
+        Vec8<TG>::load(g + s, gv);
+        Vec8<TB>::load(buf + s, v);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = momentum_update<TB>(v[q], gv[q], a.mu);
+        Vec8<TB>::store(buf + s, v);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          v[q] = 0.f;
+          if (r < a.n && c + q < a.m) {
+            const int64_t s = int64_t(r) * a.m + c + q;
+            v[q] = momentum_update<TB>(TB::load(buf, s), TG::load(g, s), a.mu);
+            TB::store(buf, s, v[q]);
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) tile[jr][seg + h * 8 + q] = TX::round(v[q]);
+    }
+  }
+  __syncthreads();
+  // phase 2: X rows i = i0 + t/4, columns j = j0 + (t%4)*16 + [0,16)
+  float ss = 0.f;
+  {
+    const int ir = threadIdx.x >> 2, seg = (threadIdx.x & 3) * 16;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        v[q] = tile[seg + h * 8 + q][ir];
+        ss += v[q] * v[q];
+      }
+      Vec8<TX>::store(x + int64_t(i0 + ir) * a.np + j0 + seg + h * 8, v);
+    }
+  }
+  const float tot = block_sum<PACK_NT>(ss, red);
+  if (threadIdx.x == 0) a.partial[int64_t(b) * a.nparts + blockIdx.x] = tot;
+}
+
+int pack_nparts(int mp, int np_, bool transposed) {
+  if (transposed) return (mp / PACK_TILE) * (np_ / PACK_TILE);
+  const int64_t total = int64_t(mp) * np_;
+  return int((total + PACK_ELEMS - 1) / PACK_ELEMS);
+}
+
+template <class TG, class TB, class TX>
+static void launch_pack_t(const PackArgs& a, bool transposed, hipStream_t s) {
+  const dim3 grid(a.nparts, a.N);
+  if (transposed)
+    hipLaunchKernelGGL((pack_cols_kernel<TG, TB, TX>), grid, dim3(PACK_NT), 0, s, a);
+  else
+    hipLaunchKernelGGL((pack_rows_kernel<TG, TB, TX>), grid, dim3(PACK_NT), 0, s, a);
+}
+
+int launch_pack(const PackArgs& a, int grad_dtype, int buf_dtype, int x_dtype, bool transposed,
+                hipStream_t s) {
+#define MMUON_PACK_CASE(GD, BD, XD, TG, TB, TX)                         \
+  if (grad_dtype == GD && buf_dtype == BD && x_dtype == XD) {           \
+    launch_pack_t<TG, TB, TX>(a, transposed, s);                        \
+    return 0;                                                           \
+  }
+  MMUON_PACK_CASE(MMUON_BF16, MMUON_F32, MMUON_BF16, BF16T, F32T, BF16T)
+  MMUON_PACK_CASE(MMUON_BF16, MMUON_BF16, MMUON_BF16, BF16T, BF16T, BF16T)
+  MMUON_PACK_CASE(MMUON_F32, MMUON_F32, MMUON_BF16, F32T, F32T, BF16T)
+  MMUON_PACK_CASE(MMUON_F32, MMUON_BF16, MMUON_BF16, F32T, BF16T, BF16T)
+  MMUON_PACK_CASE(MMUON_F32, MMUON_F32, MMUON_F32, F32T, F32T, F32T)
+  MMUON_PACK_CASE(MMUON_BF16, MMUON_F32, MMUON_F32, BF16T, F32T, F32T)
+  MMUON_PACK_CASE(MMUON_BF16, MMUON_BF16, MMUON_F32, BF16T, BF16T, F32T)
+  MMUON_PACK_CASE(MMUON_F32, MMUON_BF16, MMUON_F32, F32T, BF16T, F32T)
+#undef MMUON_PACK_CASE
+  return -1;
+}
+
+// ---------------------------------------------------------------------------
+// Per-block normalisation factor s = 1 / (||X||_F + 1e-7), from the partial sums.
+// bf16 Newton-Schulz: the reference computes the norm of the bf16 stack as a
+// bf16 tensor and adds 1e-7 in bf16 (membench monarch_muon.py:38-39), so both
+// roundings are applied here; fp32: plain fp32.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void block_scale_kernel(const float* partial, int nparts,
+                                                         float* scale, int bf16_norm) {
+  const int b = blockIdx.x;
+  float s = 0.f;
+  for (int k = threadIdx.x; k < nparts; k += 64) s += partial[int64_t(b) * nparts + k];
+  s = wave_sum(s);
+  if (threadIdx.x == 0) {
+    float nrm = sqrtf(s);
+    float d = bf16_norm ? rbf(rbf(nrm) + 1e-7f) : nrm + 1e-7f;
+    scale[b] = 1.0f / d;
+  }
+}
+
+void launch_block_scale(const float* partial, int nparts, float* scale, int N, bool bf16_norm,
+                        hipStream_t s) {
+  hipLaunchKernelGGL(block_scale_kernel, dim3(N), dim3(64), 0, s, partial, nparts, scale,
+                     bf16_norm ? 1 : 0);
+}
+
+}  // namespace mmuon

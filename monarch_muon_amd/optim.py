@@ -1,0 +1,328 @@
+"""Drop-in ``MonarchMuonOptimizer`` and ``CoatStateMonarchMuon`` on MI355X kernels.
+
+Same constructor, param groups, ``step``/``state_dict`` behaviour and state
+keys as the reference (``membench/src/models/monarch/monarch_muon.py:57-208``,
+``pretrain/src/models/monarch/monarch_muon.py:57-201``,
+``pretrain/src/models/monarch/coat_state_muon.py:117-151``).  Every step runs
+on the GPU through ``libmmuon.so``; parameters must live on a ROCm device.
+
+``ns_dtype`` selects which reference copy is reproduced:
+``torch.bfloat16`` (default) -- the membench copy: each same-shape stack is
+cast to bf16 for Newton-Schulz (the published-step-time variant);
+``None`` -- the pretrain copy: Newton-Schulz in the momentum dtype.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import _abi
+from .plan import NS_COEFFS, NS_STEPS, AdamPlanner, MuonPlanner, adamw_scalars
+
+_COEFFS = (C.c_float * 3)(*NS_COEFFS)
+
+
+def _require_gpu(t: torch.Tensor) -> None:
+    if not t.is_cuda:
+        raise RuntimeError("MonarchMuonOptimizer (MI355X) needs parameters on a ROCm GPU; "
+                           f"got a tensor on {t.device}")
+
+
+class MonarchMuonOptimizer(torch.optim.Optimizer):
+    """Muon with batched Newton-Schulz over Monarch blocks + embedded AdamW.
+
+    Group 0 (``update_type="muon"``): 3-D Monarch factors ``(nblocks, rows, cols)``.
+    Group 1 (``update_type="adamw"``): every other parameter.
+    """
+
+    def __init__(self, muon_params, adamw_params, *, lr: float = 5e-3, momentum: float = 0.95,
+                 adamw_betas: tuple = (0.9, 0.95), adamw_weight_decay: float = 0.1,
+                 adamw_eps: float = 1e-8, ns_dtype: torch.dtype | None = torch.bfloat16):
+        muon_params = list(muon_params)
+        adamw_params = list(adamw_params)
+        defaults = dict(lr=lr)
+        param_groups = [
+            {"params": muon_params, "update_type": "muon", "momentum": momentum},
+            {"params": adamw_params, "update_type": "adamw", "betas": adamw_betas,
+             "weight_decay": adamw_weight_decay, "eps": adamw_eps},
+        ]
+        super().__init__(param_groups, defaults)
+        if ns_dtype not in (torch.bfloat16, torch.float32, None):
+            raise ValueError("ns_dtype must be torch.bfloat16, torch.float32 or None")
+        self.ns_dtype = ns_dtype
+        self._muon_planner = MuonPlanner()
+        self._adam_planner = AdamPlanner()
+        self._timing = None  # optional per-launch hipEvent capture, used by bench.py
+
+    # ------------------------------------------------------------------
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        for group in self.param_groups:
+            lr = group["lr"]
+            if group["update_type"] == "muon":
+                self._muon_step(group, lr)
+            else:
+                self._adamw_step(group, lr)
+        return loss
+
+    def release_workspace(self) -> None:
+        """Drop the cached Newton-Schulz workspaces and launch tables."""
+        self._muon_planner.release()
+        self._adam_planner.release()
+
+    # ------------------------------------------------------------------
+    # Muon (membench :134-170, pretrain :133-165)
+    # ------------------------------------------------------------------
+    def _get_momentum_buffer(self, param: torch.Tensor) -> torch.Tensor:
+        state = self.state[param]
+        if "momentum_buffer" not in state:
+            state["momentum_buffer"] = torch.zeros_like(param, memory_format=torch.contiguous_format)
+        return state["momentum_buffer"]
+
+    def _muon_inputs(self, group):
+        params = [p for p in group["params"] if p.grad is not None]
+        for p in params:
+            _require_gpu(p)
+        grads = [p.grad if p.grad.is_contiguous() else p.grad.contiguous() for p in params]
+        return params, grads
+
+    def _muon_step(self, group: dict, lr: float) -> None:
+        params, grads = self._muon_inputs(group)
+        if not params:
+            return
+        bufs = [self._get_momentum_buffer(p) for p in params]
+        launches = self._muon_planner.plan(params, grads, bufs, self.ns_dtype)
+        momentum = float(group["momentum"])
+        lib = _abi.lib()
+        for gl in launches:
+            stream = _abi.stream_handle(gl.key[0])
+            ev = self._mark("pack")
+            _abi.check(lib.mmuon_momentum_pack(C.byref(gl.struct), momentum, stream), "mmuon_momentum_pack")
+            self._mark_end(ev)
+            ev = self._mark("ns", gl)
+            _abi.check(lib.mmuon_newton_schulz_apply(C.byref(gl.struct), NS_STEPS, _COEFFS,
+                                                     -lr * gl.alpha_scale, 0, stream),
+                       "mmuon_newton_schulz_apply")
+            self._mark_end(ev)
+
+    # ------------------------------------------------------------------
+    # AdamW (membench :176-208; pretrain :171-201 keeps a step per tensor)
+    # ------------------------------------------------------------------
+    def _adam_states(self, params):
+        for p in params:
+            state = self.state[p]
+            if len(state) == 0:
+                state["step"] = 0
+                state["exp_avg"] = torch.zeros_like(p, memory_format=torch.contiguous_format)
+                state["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.contiguous_format)
+            state["step"] += 1
+
+    def _adamw_step(self, group: dict, lr: float) -> None:
+        params = [p for p in group["params"] if p.grad is not None]
+        if not params:
+            return
+        for p in params:
+            _require_gpu(p)
+        self._adam_states(params)
+        grads = [p.grad if p.grad.is_contiguous() else p.grad.contiguous() for p in params]
+        ms = [self.state[p]["exp_avg"] for p in params]
+        vs = [self.state[p]["exp_avg_sq"] for p in params]
+        beta1, beta2 = group["betas"]
+        if self.ns_dtype is None:
+            steps = [self.state[p]["step"] for p in params]        # pretrain: per tensor
+        else:
+            steps = [self.state[params[0]]["step"]] * len(params)  # membench :192
+        self._launch_adamw(params, grads, ms, vs, steps, lr, beta1, beta2, group["eps"],
+                           group["weight_decay"])
+
+    def _launch_adamw(self, params, grads, ms, vs, steps, lr, beta1, beta2, eps, wd, fp8_meta=None):
+        launches = self._adam_planner.plan(params, grads, ms, vs, fp8_meta)
+        lib = _abi.lib()
+        for al in launches:
+            step_values = sorted({steps[i] for i in al.members})
+            if len(step_values) != 1:
+                # tensors whose step counts differ: one launch per step value
+                self._adamw_split(al, params, grads, ms, vs, steps, lr, beta1, beta2, eps, wd, fp8_meta)
+                continue
+            self._adamw_one(lib, al, step_values[0], lr, beta1, beta2, eps, wd)
+
+    def _adamw_one(self, lib, al, step, lr, beta1, beta2, eps, wd):
+        args = _abi.AdamWArgs(tensors=al.tensors.data_ptr(), chunks=al.chunks.data_ptr(), nchunks=al.nchunks,
+                              chunk_elems=al.chunk, param_dtype=_abi.dtype_code(al.pd),
+                              grad_dtype=_abi.dtype_code(al.gd), state_dtype=_abi.dtype_code(al.sd),
+                              **adamw_scalars(lr, beta1, beta2, eps, wd, step))
+        stream = _abi.stream_handle(al.tensors.device)
+        ev = self._mark("adamw")
+        if al.fp8 is not None:
+            _abi.check(lib.mmuon_adamw_fp8(C.byref(args), C.cast(al.fp8.data_ptr(), C.POINTER(_abi.AdamWFp8Tensor)),
+                                           1, stream), "mmuon_adamw_fp8")
+        else:
+            _abi.check(lib.mmuon_adamw(C.byref(args), stream), "mmuon_adamw")
+        self._mark_end(ev)
+
+    def _adamw_split(self, al, params, grads, ms, vs, steps, lr, beta1, beta2, eps, wd, fp8_meta):
+        lib = _abi.lib()
+        by_step: dict = {}
+        for i in al.members:
+            by_step.setdefault(steps[i], []).append(i)
+        for step, idx in by_step.items():
+            sub = AdamPlanner().plan([params[i] for i in idx], [grads[i] for i in idx], [ms[i] for i in idx],
+                                     [vs[i] for i in idx], [fp8_meta[i] for i in idx] if fp8_meta else None)
+            for sl in sub:
+                self._adamw_one(lib, sl, step, lr, beta1, beta2, eps, wd)
+
+    # ------------------------------------------------------------------
+    # optional per-launch timing (bench.py): hipEvents on the launch stream
+    # ------------------------------------------------------------------
+    def _mark(self, name, gl=None):
+        if self._timing is None:
+            return None
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        return (name, gl, s, e)
+
+    def _mark_end(self, ev):
+        if ev is None:
+            return
+        ev[3].record()
+        self._timing.append(ev)
+
+
+# ---------------------------------------------------------------------------
+# FP8 optimizer states (coat_state_muon.py:117-151)
+# ---------------------------------------------------------------------------
+STATES = {"momentum_buffer": True, "exp_avg": True, "exp_avg_sq": False}   # name -> signed
+_FP8 = {"E4M3": torch.float8_e4m3fn}
+
+
+class QuantizationConfig:
+    """The optimizer-state fields of COAT's ``QuantizationConfig``
+    (``third_party/coat/utils/_fp8_quantization_config.py:20-26``)."""
+
+    def __init__(self, first_order_expansion="true", second_order_expansion="true",
+                 first_order_bit="E4M3", second_order_bit="E4M3", qgroup_size=128, expand_min=16, **_):
+        self.first_order_expansion = first_order_expansion
+        self.second_order_expansion = second_order_expansion
+        self.first_order_bit = first_order_bit
+        self.second_order_bit = second_order_bit
+        self.qgroup_size = qgroup_size
+        self.expand_min = expand_min
+
+
+class CoatStateMonarchMuon(MonarchMuonOptimizer):
+    """Every optimizer state stored as e4m3 in groups of 128 with dynamic range
+    expansion; each step dequantizes, updates and requantizes inside the fused
+    kernels (no fp32 copy of any state is materialised)."""
+
+    def __init__(self, *args, qargs, **kwargs):
+        if qargs.qgroup_size != 128:
+            raise AssertionError("COAT's optimizer kernels use groups of 128")
+        if qargs.first_order_expansion not in ("expand", "true") or qargs.second_order_expansion not in ("expand", "true"):
+            raise AssertionError("only the dynamic-range-expansion codec is supported")
+        for bit in (qargs.first_order_bit, qargs.second_order_bit):
+            if bit not in _FP8:
+                raise NotImplementedError(f"FP8 state format {bit} (only E4M3 is implemented)")
+        if int(qargs.expand_min) != 16:
+            raise NotImplementedError("expand_min other than 16")
+        self.dtypes = {name: _FP8[qargs.first_order_bit] for name in ("momentum_buffer", "exp_avg")}
+        self.dtypes["exp_avg_sq"] = _FP8[qargs.second_order_bit]
+        self.expand_min = qargs.expand_min
+        super().__init__(*args, **kwargs)
+
+    @staticmethod
+    def _ensure_fp8(state, name, like):
+        """FP8 payload + metadata for ``state[name]``; a missing state starts as
+        exact zeros (codes 0 decode to 0 whatever the metadata)."""
+        groups = (like.numel() + 127) // 128
+        cur = state.get(name)
+        if cur is None or cur.dtype != torch.float8_e4m3fn:
+            if cur is None:
+                state[name] = torch.zeros(like.shape, dtype=torch.float8_e4m3fn, device=like.device)
+                for key in ("scale", "expand", "sqrt_minmax"):
+                    state[f"{key}_{name}"] = torch.ones(groups, dtype=torch.float32, device=like.device)
+            else:
+                # a floating state (e.g. restored without its FP8 dtype): quantize it
+                value = cur.detach().to(torch.float32).contiguous()
+                codes = torch.empty(like.shape, dtype=torch.float8_e4m3fn, device=like.device)
+                meta = [torch.empty(groups, dtype=torch.float32, device=like.device) for _ in range(3)]
+                _abi.fp8_quantize(value, codes.view(torch.uint8), *meta, signed=STATES[name])
+                state[name] = codes
+                for key, t in zip(("scale", "expand", "sqrt_minmax"), meta):
+                    state[f"{key}_{name}"] = t
+        for key in ("scale", "expand", "sqrt_minmax"):
+            t = state[f"{key}_{name}"]
+            if t.dtype != torch.float32:
+                state[f"{key}_{name}"] = t.to(torch.float32)
+        return state[name]
+
+    def _meta(self, state, name):
+        return tuple(state[f"{key}_{name}"] for key in ("scale", "expand", "sqrt_minmax"))
+
+    def _muon_step(self, group: dict, lr: float) -> None:
+        params, grads = self._muon_inputs(group)
+        if not params:
+            return
+        bufs = [self._ensure_fp8(self.state[p], "momentum_buffer", p) for p in params]
+        for p in params:
+            if (p.numel() // p.shape[0]) % 128 != 0:
+                raise NotImplementedError("FP8 momentum needs rows*cols % 128 == 0 for every Monarch block")
+        meta = [self._meta(self.state[p], "momentum_buffer") for p in params]
+        launches = self._muon_planner.plan(params, grads, bufs, self.ns_dtype, fp8_meta=meta)
+        momentum = float(group["momentum"])
+        lib = _abi.lib()
+        for gl in launches:
+            stream = _abi.stream_handle(gl.key[0])
+            ev = self._mark("pack")
+            _abi.check(lib.mmuon_fp8_momentum_pack(C.byref(gl.struct), momentum, 1, stream),
+                       "mmuon_fp8_momentum_pack")
+            self._mark_end(ev)
+            ev = self._mark("ns", gl)
+            _abi.check(lib.mmuon_newton_schulz_apply(C.byref(gl.struct), NS_STEPS, _COEFFS,
+                                                     -lr * gl.alpha_scale, 0, stream),
+                       "mmuon_newton_schulz_apply")
+            self._mark_end(ev)
+
+    def _adamw_step(self, group: dict, lr: float) -> None:
+        params = [p for p in group["params"] if p.grad is not None]
+        if not params:
+            return
+        for p in params:
+            _require_gpu(p)
+            state = self.state[p]
+            if "step" not in state:
+                state["step"] = 0
+            state["step"] += 1
+            self._ensure_fp8(state, "exp_avg", p)
+            self._ensure_fp8(state, "exp_avg_sq", p)
+        grads = [p.grad if p.grad.is_contiguous() else p.grad.contiguous() for p in params]
+        ms = [self.state[p]["exp_avg"] for p in params]
+        vs = [self.state[p]["exp_avg_sq"] for p in params]
+        meta = [self._meta(self.state[p], "exp_avg") + self._meta(self.state[p], "exp_avg_sq") for p in params]
+        beta1, beta2 = group["betas"]
+        if self.ns_dtype is None:
+            steps = [self.state[p]["step"] for p in params]
+        else:
+            steps = [self.state[params[0]]["step"]] * len(params)
+        self._launch_adamw(params, grads, ms, vs, steps, lr, beta1, beta2, group["eps"],
+                           group["weight_decay"], fp8_meta=meta)
+
+    def load_state_dict(self, state_dict):
+        # torch.optim casts floating state to the parameter dtype; put the FP8
+        # payloads (exact in any wider float) and fp32 metadata back.
+        saved = {key: {name: value.dtype for name, value in entry.items() if name in STATES}
+                 for key, entry in state_dict["state"].items()}
+        super().load_state_dict(state_dict)
+        params = [p for group in self.param_groups for p in group["params"]]
+        for key, dtypes in saved.items():
+            state = self.state[params[key]]
+            for name, dtype in dtypes.items():
+                state[name] = state[name].to(dtype)
+                for meta in ("scale", "expand", "sqrt_minmax"):
+                    mk = f"{meta}_{name}"
+                    if mk in state and state[mk].dtype != torch.float32:
+                        state[mk] = state[mk].to(torch.float32)

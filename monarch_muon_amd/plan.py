@@ -1,0 +1,246 @@
+"""Grouping and launch planner for the Monarch-Muon step.
+
+The reference buckets the Muon parameters by ``(device, dtype, rows, cols)`` of
+their momentum buffers, in first-appearance order, and concatenates each
+bucket's blocks in parameter order (membench ``monarch_muon.py:153-161``).  The
+planner reproduces that order exactly, but instead of copying the buffers into
+a stack it builds a device table with one ``(param, grad, buf)`` pointer triple
+per Monarch block; the fused pack kernel reads the blocks in place.  Tables and
+workspaces are cached and rebuilt only when a pointer, dtype or shape changes.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from collections import OrderedDict
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _abi
+
+NS_COEFFS = (3.4445, -4.7750, 2.0315)   # membench monarch_muon.py:47
+NS_STEPS = 5                            # membench monarch_muon.py:45
+
+
+def group_key(buf: torch.Tensor):
+    """``(device, dtype, rows, cols)`` of a momentum buffer (membench :156)."""
+    return (buf.device, buf.dtype, buf.shape[1], buf.shape[2])
+
+
+def plan_groups(bufs) -> "OrderedDict[tuple, list[int]]":
+    """Indices of ``bufs`` per group key, keys in first-appearance order."""
+    groups: "OrderedDict[tuple, list[int]]" = OrderedDict()
+    for i, buf in enumerate(bufs):
+        if buf.dim() != 3:
+            raise ValueError(f"Muon parameters must be 3-D (nblocks, rows, cols); got shape {tuple(buf.shape)}")
+        groups.setdefault(group_key(buf), []).append(i)
+    return groups
+
+
+def _h2d_int64(values, device) -> torch.Tensor:
+    host = torch.tensor(values, dtype=torch.int64).pin_memory()
+    return host.to(device, non_blocking=True)
+
+
+@dataclass
+class Workspace:
+    """Newton-Schulz workspace of one group geometry (owned by torch)."""
+    layout: _abi.NsLayout
+    x0: torch.Tensor
+    x1: torch.Tensor
+    a: torch.Tensor
+    p: torch.Tensor
+    partial: torch.Tensor
+    scale: torch.Tensor
+
+    @classmethod
+    def allocate(cls, rows, cols, ns_code, nblocks, device) -> "Workspace":
+        lay = _abi.ns_layout(rows, cols, ns_code, nblocks)
+        u8 = dict(dtype=torch.uint8, device=device)
+        return cls(lay, torch.zeros(lay.x_bytes, **u8), torch.zeros(lay.x_bytes, **u8),
+                   torch.empty(lay.a_bytes, **u8), torch.empty(lay.a_bytes, **u8),
+                   torch.empty(max(lay.part_bytes, 4), **u8),
+                   torch.empty(nblocks, dtype=torch.float32, device=device))
+
+    def x_view(self, which: int, dtype: torch.dtype, nblocks: int) -> torch.Tensor:
+        """The X stack ``[N, mp, np]`` (``which`` = 0 or 1) as a typed view."""
+        t = self.x0 if which == 0 else self.x1
+        return t.view(dtype).view(nblocks, self.layout.mp, self.layout.np_)
+
+
+@dataclass
+class GroupLaunch:
+    key: tuple
+    rows: int
+    cols: int
+    nblocks: int
+    members: list                 # indices into the step's param list, in order
+    ws: Workspace
+    table: torch.Tensor           # device int64 [N, 3]
+    fp8_table: torch.Tensor | None
+    struct: _abi.Group = field(default_factory=_abi.Group)
+
+    @property
+    def alpha_scale(self) -> float:
+        return (self.rows / self.cols) ** 0.5   # membench :167
+
+    @property
+    def transposed(self) -> bool:
+        return self.rows > self.cols
+
+
+class MuonPlanner:
+    """Builds and caches the per-step launch plan of the Muon group."""
+
+    def __init__(self):
+        self._sig = None
+        self._groups: list[GroupLaunch] = []
+        self._ws: dict = {}
+
+    @property
+    def groups(self) -> list[GroupLaunch]:
+        return self._groups
+
+    def release(self) -> None:
+        self._sig = None
+        self._groups = []
+        self._ws = {}
+
+    def plan(self, params, grads, bufs, ns_dtype: torch.dtype, fp8_meta=None) -> list[GroupLaunch]:
+        sig = tuple((p.data_ptr(), g.data_ptr(), b.data_ptr(), p.dtype, g.dtype, b.dtype, tuple(b.shape))
+                    for p, g, b in zip(params, grads, bufs))
+        if fp8_meta is not None:
+            sig = sig + tuple(m[0].data_ptr() for m in fp8_meta)
+        if sig == self._sig:
+            return self._groups
+        self._groups = [self._build(key, idx, params, grads, bufs, ns_dtype, fp8_meta)
+                        for key, idx in plan_groups(bufs).items()]
+        self._sig = sig
+        return self._groups
+
+    def _workspace(self, rows, cols, ns_code, nblocks, device) -> Workspace:
+        k = (rows, cols, ns_code, nblocks, device)
+        ws = self._ws.get(k)
+        if ws is None:
+            ws = self._ws[k] = Workspace.allocate(rows, cols, ns_code, nblocks, device)
+        return ws
+
+    def _build(self, key, idx, params, grads, bufs, ns_dtype, fp8_meta) -> GroupLaunch:
+        device, bdtype, rows, cols = key
+        rc = rows * cols
+        pd, gd = params[idx[0]].dtype, grads[idx[0]].dtype
+        for i in idx:
+            p, g, b = params[i], grads[i], bufs[i]
+            if p.dtype != pd or g.dtype != gd:
+                raise TypeError("parameters (and their grads) of one block shape must share a dtype")
+            if not (p.is_contiguous() and g.is_contiguous() and b.is_contiguous()):
+                raise ValueError("Muon parameters, grads and momentum buffers must be contiguous")
+            if p.shape != b.shape or g.shape != p.shape:
+                raise ValueError("param, grad and momentum shapes differ")
+        if ns_dtype is not None:
+            ns_code = _abi.dtype_code(ns_dtype)
+        elif bdtype == torch.float8_e4m3fn:
+            ns_code = _abi.F32          # the FP8 reference dequantizes the momentum to fp32
+        else:
+            ns_code = _abi.dtype_code(bdtype)
+        nblocks = sum(bufs[i].shape[0] for i in idx)
+        ws = self._workspace(rows, cols, ns_code, nblocks, device)
+        es_p, es_g, es_b = params[idx[0]].element_size(), grads[idx[0]].element_size(), bufs[idx[0]].element_size()
+        rows_tab, rows_fp8 = [], []
+        aligned = True
+        for i in idx:
+            pp, gp, bp = params[i].data_ptr(), grads[i].data_ptr(), bufs[i].data_ptr()
+            for k in range(bufs[i].shape[0]):
+                trip = (pp + k * rc * es_p, gp + k * rc * es_g, bp + k * rc * es_b)
+                aligned = aligned and all(v % 16 == 0 for v in trip)
+                rows_tab.append(trip)
+                if fp8_meta is not None:
+                    gpb = rc // 128
+                    rows_fp8.append(tuple(m.data_ptr() + k * gpb * 4 for m in fp8_meta[i]))
+        table = _h2d_int64(rows_tab, device)
+        fp8_table = _h2d_int64(rows_fp8, device) if fp8_meta is not None else None
+        gl = GroupLaunch(key, rows, cols, nblocks, list(idx), ws, table, fp8_table)
+        s = gl.struct
+        s.rows, s.cols, s.nblocks = rows, cols, nblocks
+        s.param_dtype, s.grad_dtype = _abi.dtype_code(pd), _abi.dtype_code(gd)
+        s.buf_dtype = _abi.dtype_code(bdtype)
+        s.ns_dtype = ns_code
+        s.flags = _abi.GROUP_ALIGNED16 if aligned else 0
+        s.blocks = table.data_ptr()
+        s.fp8 = fp8_table.data_ptr() if fp8_table is not None else None
+        s.x0, s.x1 = ws.x0.data_ptr(), ws.x1.data_ptr()
+        s.a, s.p = ws.a.data_ptr(), ws.p.data_ptr()
+        s.partial, s.scale = ws.partial.data_ptr(), ws.scale.data_ptr()
+        return gl
+
+
+# ---------------------------------------------------------------------------
+# AdamW group
+# ---------------------------------------------------------------------------
+ADAM_CHUNK = 8192
+
+
+@dataclass
+class AdamLaunch:
+    members: list                 # indices into the step's param list
+    pd: torch.dtype
+    gd: torch.dtype
+    sd: torch.dtype
+    tensors: torch.Tensor         # device int64 [T, 5]
+    chunks: torch.Tensor          # device int64 [nchunks]
+    nchunks: int
+    chunk: int
+    fp8: torch.Tensor | None = None  # device int64 [T, 6]
+
+
+class AdamPlanner:
+    def __init__(self):
+        self._sig = None
+        self._launches: list[AdamLaunch] = []
+
+    def release(self) -> None:
+        self._sig = None
+        self._launches = []
+
+    def plan(self, params, grads, ms, vs, fp8_meta=None) -> list[AdamLaunch]:
+        sig = tuple((p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), p.dtype, g.dtype, m.dtype, p.numel())
+                    for p, g, m, v in zip(params, grads, ms, vs))
+        if fp8_meta is not None:
+            sig = sig + tuple(t.data_ptr() for meta in fp8_meta for t in meta)
+        if sig == self._sig:
+            return self._launches
+        buckets: "OrderedDict[tuple, list[int]]" = OrderedDict()
+        for i, (p, g, m, v) in enumerate(zip(params, grads, ms, vs)):
+            if m.dtype != v.dtype:
+                raise TypeError("exp_avg and exp_avg_sq must share a dtype")
+            for t in (p, g, m, v):
+                if not t.is_contiguous():
+                    raise ValueError("AdamW parameters, grads and states must be contiguous")
+            buckets.setdefault((p.device, p.dtype, g.dtype, m.dtype), []).append(i)
+        launches = []
+        chunk = 128 if fp8_meta is not None else ADAM_CHUNK
+        for (device, pd, gd, sd), idx in buckets.items():
+            tens, chunks, f8 = [], [], []
+            for t, i in enumerate(idx):
+                n = params[i].numel()
+                tens.append((params[i].data_ptr(), grads[i].data_ptr(), ms[i].data_ptr(), vs[i].data_ptr(), n))
+                chunks.extend((t << 40) | s for s in range(0, n, chunk))
+                if fp8_meta is not None:
+                    f8.append(tuple(x.data_ptr() for x in fp8_meta[i]))
+            launches.append(AdamLaunch(
+                idx, pd, gd, sd, _h2d_int64(tens, device), _h2d_int64(chunks or [0], device), len(chunks), chunk,
+                _h2d_int64(f8, device) if fp8_meta is not None else None))
+        self._launches = launches
+        self._sig = sig
+        return launches
+
+
+def adamw_scalars(lr, beta1, beta2, eps, weight_decay, step) -> dict:
+    """Scalars exactly as the reference forms them in Python doubles
+    (membench monarch_muon.py:196-208)."""
+    bc1 = 1.0 - beta1 ** step
+    bc2 = 1.0 - beta2 ** step
+    return dict(apply_weight_decay=int(weight_decay > 0), wd_factor=1.0 - lr * weight_decay,
+                beta1=beta1, beta2=beta2, one_minus_beta1=1.0 - beta1, one_minus_beta2=1.0 - beta2,
+                sqrt_bc2=math.sqrt(bc2), eps=eps, neg_step_size=-lr / bc1)

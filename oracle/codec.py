@@ -1,0 +1,153 @@
+"""numpy restatement of the FP8 optimizer-state codec -- test infrastructure.
+
+Restates ``pretrain/src/models/monarch/coat_state_muon.py``:
+``_quantize_kernel`` (``:46-91``) and ``_dequantize_kernel`` (``:22-43``), with
+the constants of ``third_party/coat/utils/_fp8_quantization_config.py:20-26``
+(group 128, E4M3, expand_min 16).  Each group of 128 consecutive elements of
+the flattened tensor (the last group may be short) carries three fp32 values:
+``scale``, ``expand`` and ``sqrt_minmax``.
+
+All arithmetic is float32 with correctly rounded operations (numpy float32),
+``pow``/``log2`` from the C library.  The reference's Triton kernels use
+approximate division/sqrt and CUDA libdevice ``pow``; bit equality with them
+is not claimed.  Pinning: ``tests/test_oracle.py`` checks the round-trip error
+bound of e4m3, the constant-group and zero-group special cases, the exact
+halving invariant of ``test_coat_state_muon.py:40-51`` and the e4m3 encoder
+against torch's ``float8_e4m3fn`` cast.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+GROUP = 128          # coat_state_muon.py:16
+FP8_MAX = 448.0      # torch.finfo(float8_e4m3fn).max, coat_state_muon.py:113
+EXPAND_MIN = 16      # _fp8_quantization_config.py:26
+QUANT_EPS = np.float32(1e-30)
+F32 = np.float32
+
+
+def e4m3_encode(x: np.ndarray) -> np.ndarray:
+    """fp32 -> OCP e4m3fn byte, round-to-nearest-even, saturating to +-448.
+
+    Pure integer restatement of IEEE rounding (no library cast), so it can pin
+    the HIP encoder bit for bit."""
+    x = np.asarray(x, dtype=np.float32)
+    bits = x.view(np.uint32).astype(np.int64)
+    sign = ((bits >> 31) & 1).astype(np.uint8) << 7
+    a = np.abs(x).astype(np.float32)
+    out = np.zeros(x.shape, dtype=np.uint8)
+    nan = np.isnan(a)
+    a = np.where(nan, 0, np.minimum(a, FP8_MAX)).astype(np.float32)
+    ab = a.view(np.uint32).astype(np.int64)
+    exp = (ab >> 23) - 127
+    man = ab & 0x7FFFFF
+    # normal e4m3: exponent -6..8 (bias 7), 3 mantissa bits
+    normal = exp >= -6
+    # round mantissa 23 -> 3 bits, RNE
+    shift = 20
+    m_full = man | 0x800000
+    q = m_full >> shift
+    rem = m_full & ((1 << shift) - 1)
+    half = 1 << (shift - 1)
+    q = q + ((rem > half) | ((rem == half) & (q & 1 == 1)))
+    e_n = exp + 7
+    carry = q >= 16
+    q = np.where(carry, q >> 1, q)
+    e_n = np.where(carry, e_n + 1, e_n)
+    code_n = (e_n << 3) | (q & 7)
+    # subnormal: value = k * 2^-9, k = 0..7 (8 rounds up to the min normal)
+    scaled = a.astype(np.float64) * 512.0            # exact in fp64
+    k = np.floor(scaled)
+    frac = scaled - k
+    k = k + ((frac > 0.5) | ((frac == 0.5) & (np.mod(k, 2) == 1)))
+    code_s = k.astype(np.int64)                       # k == 8 -> 0x08 = min normal, correct
+    code = np.where(normal, code_n, code_s)
+    code = np.where(a == 0, 0, code)
+    out = (code.astype(np.uint8) | sign)
+    out = np.where(nan, np.uint8(0x7F) | sign, out)
+    return out.astype(np.uint8)
+
+
+def e4m3_decode(code: np.ndarray) -> np.ndarray:
+    """OCP e4m3fn byte -> fp32 (exact)."""
+    c = np.asarray(code, dtype=np.uint8).astype(np.int64)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 0xF
+    m = c & 7
+    val = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    val = np.where((c & 0x7F) == 0x7F, np.nan, val)
+    return (sign * val).astype(np.float32)
+
+
+def _groups(flat: np.ndarray):
+    n = flat.size
+    ngroups = (n + GROUP - 1) // GROUP
+    padded = np.zeros(ngroups * GROUP, dtype=np.float32)
+    padded[:n] = flat
+    mask = np.zeros(ngroups * GROUP, dtype=bool)
+    mask[:n] = True
+    return padded.reshape(ngroups, GROUP), mask.reshape(ngroups, GROUP), n
+
+
+def quantize(value: np.ndarray, signed: bool, fp8_max: float = FP8_MAX,
+             expand_min: int = EXPAND_MIN):
+    """Restates ``_quantize_kernel`` (``coat_state_muon.py:46-91``).
+
+    Returns ``(codes uint8 [numel], scale f32 [G], expand f32 [G],
+    sqrt_minmax f32 [G])``."""
+    flat = np.asarray(value, dtype=np.float32).reshape(-1)
+    m, mask, n = _groups(flat)
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        abs_m = np.abs(m)
+        valid = mask & (abs_m > 0)
+        absmax = np.max(np.where(mask, abs_m, F32(0)), axis=1)
+        absmin = np.min(np.where(valid, abs_m, F32(3.4028235e38)), axis=1)
+        nonzero = valid.sum(axis=1)
+        absmax = np.maximum(absmax, QUANT_EPS)
+        absmin = np.where(nonzero > 0, np.maximum(absmin, QUANT_EPS), QUANT_EPS).astype(F32)
+        ratio = (absmax / absmin).astype(F32)
+        ratio = np.maximum(ratio, F32(1.0) + QUANT_EPS)          # 1 + 1e-30 == 1 in f32
+        ratio_upper = F32(fp8_max) * F32(fp8_max) / F32(2.0)
+        log_ratio = np.log2(ratio).astype(F32)
+        safe_log = np.where(log_ratio > QUANT_EPS, log_ratio, F32(1.0)).astype(F32)
+        em = F32(expand_min)
+        raw_expand = (np.floor((np.log2(ratio_upper).astype(F32) / safe_log) * em) / em).astype(F32)
+        expand = np.where(ratio <= F32(1.0) + QUANT_EPS, F32(1.0),
+                          np.maximum(raw_expand, F32(1.0) / em)).astype(F32)
+        sqrt_minmax = (np.sqrt(absmax) * np.sqrt(absmin)).astype(F32)
+        sqrt_minmax = np.maximum(sqrt_minmax, QUANT_EPS)
+        norm_base = np.maximum(abs_m / sqrt_minmax[:, None], QUANT_EPS).astype(F32)
+        norm_pow = np.power(norm_base, expand[:, None]).astype(F32)
+        if signed:
+            sgn = np.where(m >= 0, F32(1.0), F32(-1.0))
+            normalized = np.where(mask & (abs_m > 0), sgn * norm_pow, F32(0)).astype(F32)
+        else:
+            normalized = np.where(mask & (abs_m > 0), norm_pow, F32(0)).astype(F32)
+        scale_base = np.maximum(absmax / sqrt_minmax, QUANT_EPS).astype(F32)
+        scale = (np.power(scale_base, expand).astype(F32) / F32(fp8_max)).astype(F32)
+        scale = np.maximum(scale, QUANT_EPS)
+        q = (normalized / scale[:, None]).astype(F32)
+    codes = e4m3_encode(q).reshape(-1)[:n]
+    return codes, scale.astype(F32), expand.astype(F32), sqrt_minmax.astype(F32)
+
+
+def dequantize(codes: np.ndarray, scale, expand, sqrt_minmax, signed: bool) -> np.ndarray:
+    """Restates ``_dequantize_kernel`` (``coat_state_muon.py:22-43``)."""
+    flat = e4m3_decode(np.asarray(codes).reshape(-1))
+    raw, mask, n = _groups(flat)
+    s = np.asarray(scale, dtype=F32)[:, None]
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        ex = np.maximum(np.asarray(expand, dtype=F32), QUANT_EPS)[:, None]
+        smm = np.maximum(np.asarray(sqrt_minmax, dtype=F32), QUANT_EPS)[:, None]
+        inv = (F32(1.0) / ex).astype(F32)
+        if signed:
+            scaled = (raw * s).astype(F32)
+            absolute = np.abs(scaled)
+            sgn = np.where(scaled >= 0, F32(1.0), F32(-1.0))
+            power = np.power(np.maximum(absolute, QUANT_EPS), inv).astype(F32)
+            value = np.where(absolute > 0, (sgn * power).astype(F32) * smm, F32(0)).astype(F32)
+        else:
+            scaled = np.maximum((raw * s).astype(F32), F32(0))
+            power = np.power(np.maximum(scaled, QUANT_EPS), inv).astype(F32)
+            value = np.where(scaled > 0, power * smm, F32(0)).astype(F32)
+    return value.reshape(-1)[:n]

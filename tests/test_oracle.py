@@ -1,0 +1,243 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the parity checker.
+
+Each check is chosen so a plausible restatement mistake (dropped term, wrong
+sign, transposed operand, wrong rounding point) fails it.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from golden_inputs import CASES, input_checksum, make_case
+from oracle import codec, shapes
+from oracle.step import NS_COEFFS, ReferenceMonarchMuon, group_blocks, newton_schulz_batched
+from oracle.truth import known_answer, ns_fp64, quintic_scalar, rel_fro
+
+GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+
+
+# ---------------------------------------------------------------- golden vectors
+@pytest.mark.parametrize("case", CASES, ids=[c["name"] for c in CASES])
+def test_oracle_matches_reference_golden(case):
+    gold = torch.load(GOLDEN / f"{case['name']}.pt", weights_only=True)
+    assert gold["inputs_sha"] == input_checksum(case), "seeded input generator drifted"
+    muon, adamw, bufs = make_case(case)
+    opt = ReferenceMonarchMuon(muon, adamw, lr=case["lr"], momentum=0.95, variant=case["variant"])
+    if bufs is not None:
+        for p, b in zip(muon, bufs):
+            opt.state[p]["momentum_buffer"] = b
+    for _ in range(case["steps"]):
+        opt.step()
+    tol = dict(rtol=1e-6, atol=1e-9)
+    for p, q in zip(muon, gold["muon_params"]):
+        torch.testing.assert_close(p.detach(), q, **tol)
+    for p, q in zip(muon, gold["momentum"]):
+        torch.testing.assert_close(opt.state[p]["momentum_buffer"], q, **tol)
+    for p, q in zip(adamw, gold["adamw_params"]):
+        torch.testing.assert_close(p.detach(), q, **tol)
+    for p, q, r in zip(adamw, gold["exp_avg"], gold["exp_avg_sq"]):
+        torch.testing.assert_close(opt.state[p]["exp_avg"], q, **tol)
+        torch.testing.assert_close(opt.state[p]["exp_avg_sq"], r, **tol)
+    torch.testing.assert_close(newton_schulz_batched(gold["ns_input"]), gold["ns_output"], rtol=0, atol=0)
+
+
+# ---------------------------------------------------------------- Newton-Schulz
+def _svd_case(r, c, seed):
+    g = torch.Generator().manual_seed(seed)
+    k = min(r, c)
+    u, _ = torch.linalg.qr(torch.randn(r, k, generator=g, dtype=torch.float64))
+    v, _ = torch.linalg.qr(torch.randn(c, k, generator=g, dtype=torch.float64))
+    s = torch.rand(k, generator=g, dtype=torch.float64) * 2 + 0.01
+    return u, s, v, (u * s) @ v.T
+
+
+@pytest.mark.parametrize("r,c", [(24, 24), (40, 16), (16, 40)])
+def test_ns_known_answer_svd(r, c):
+    u, s, v, x = _svd_case(r, c, 3)
+    out = newton_schulz_batched(x[None])[0]
+    ref = known_answer(u, s, v)
+    assert rel_fro(out, ref) < 1e-12
+    # the scalar quintic is what acts on each singular value
+    sv = torch.linalg.svdvals(out).sort().values
+    phi = torch.from_numpy(np.sort(quintic_scalar((s / (s.norm() + 1e-7)).numpy())))
+    torch.testing.assert_close(sv, phi, rtol=1e-10, atol=1e-12)
+
+
+def test_ns_diagonal_exact():
+    d = torch.diag(torch.tensor([3.0, 1.0, 0.5, 0.25], dtype=torch.float64))
+    out = newton_schulz_batched(d[None])[0]
+    expect = quintic_scalar((torch.diagonal(d) / (torch.diagonal(d).norm() + 1e-7)).numpy())
+    torch.testing.assert_close(torch.diagonal(out), torch.from_numpy(expect))
+    assert torch.count_nonzero(out - torch.diag(torch.diagonal(out))) == 0
+
+
+def test_ns_invariants():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(20, 33, generator=g, dtype=torch.float64)
+    q, _ = torch.linalg.qr(torch.randn(20, 20, generator=g, dtype=torch.float64))
+    rr, _ = torch.linalg.qr(torch.randn(33, 33, generator=g, dtype=torch.float64))
+    f = lambda t: newton_schulz_batched(t[None])[0]
+    torch.testing.assert_close(f(q @ x @ rr), q @ f(x) @ rr, rtol=1e-9, atol=1e-10)
+    torch.testing.assert_close(f(x.T), f(x).T, rtol=1e-12, atol=1e-13)
+    # equal up to the 1e-7 in the normaliser, amplified by the quintic slope (~3.4445^5)
+    torch.testing.assert_close(f(7.5 * x), f(x), rtol=1e-4, atol=1e-7)
+    assert torch.count_nonzero(f(torch.zeros(5, 9, dtype=torch.float64))) == 0
+
+
+def test_ns_matches_fp64_three_product_form_in_fp64():
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(3, 24, 40, generator=g, dtype=torch.float64)
+    assert rel_fro(newton_schulz_batched(x), ns_fp64(x)).max() < 1e-12
+
+
+def test_ns_coefficients_are_the_reference_quintic():
+    # phi(x) = a x + b x^3 + c x^5 with a + b + c = 0.7010 (not a fixed point at 1 on purpose)
+    a, b, c = NS_COEFFS
+    assert (a, b, c) == (3.4445, -4.7750, 2.0315)
+    assert quintic_scalar(np.array([0.0]))[0] == 0.0
+
+
+# ---------------------------------------------------------------- momentum / apply
+def test_momentum_and_apply_brute_force_fp64():
+    g = torch.Generator().manual_seed(7)
+    w = (torch.randn(2, 8, 12, generator=g) * 0.02)
+    gr = torch.randn(2, 8, 12, generator=g) * 1e-3
+    buf = torch.randn(2, 8, 12, generator=g) * 1e-3
+    p = w.clone().requires_grad_(True)
+    p.grad = gr.clone()
+    opt = ReferenceMonarchMuon([p], [], lr=0.05, momentum=0.9, variant="pretrain")
+    opt.state[p]["momentum_buffer"] = buf.clone()
+    opt.step()
+    # two fp32 roundings (mul_ then add_), no fused multiply-add
+    nb32 = (buf.numpy() * np.float32(0.9)).astype(np.float32) + gr.numpy()
+    np.testing.assert_array_equal(opt.state[p]["momentum_buffer"].numpy(), nb32)
+    nb = 0.9 * buf.double() + gr.double()
+    torch.testing.assert_close(opt.state[p]["momentum_buffer"].double(), nb, rtol=0, atol=1e-9)
+    upd = ns_fp64(nb)
+    expect = w.double() - 0.05 * math.sqrt(8 / 12) * upd
+    torch.testing.assert_close(p.detach().double(), expect, rtol=1e-5, atol=1e-7)
+
+
+def test_grad_none_is_skipped_and_zero_grad_gives_zero_update():
+    p = torch.randn(1, 8, 8).requires_grad_(True)
+    q = torch.randn(1, 8, 8).requires_grad_(True)
+    q.grad = torch.zeros_like(q)
+    p0, q0 = p.detach().clone(), q.detach().clone()
+    opt = ReferenceMonarchMuon([p, q], [], variant="membench")
+    opt.step()
+    assert torch.equal(p.detach(), p0) and "momentum_buffer" not in opt.state[p]
+    assert torch.equal(q.detach(), q0)
+
+
+# ---------------------------------------------------------------- AdamW
+@pytest.mark.parametrize("variant", ["membench", "pretrain"])
+def test_adamw_matches_torch_adamw(variant):
+    g = torch.Generator().manual_seed(8)
+    ws = [torch.randn(17, 5, generator=g, dtype=torch.float64), torch.randn(9, generator=g, dtype=torch.float64)]
+    a = [w.clone().requires_grad_(True) for w in ws]
+    b = [w.clone().requires_grad_(True) for w in ws]
+    ours = ReferenceMonarchMuon([], a, lr=1e-2, adamw_betas=(0.9, 0.95), adamw_weight_decay=0.1,
+                                adamw_eps=1e-8, variant=variant)
+    lib = torch.optim.AdamW(b, lr=1e-2, betas=(0.9, 0.95), weight_decay=0.1, eps=1e-8, foreach=False)
+    for step in range(3):
+        grads = [torch.randn(w.shape, generator=g, dtype=torch.float64) for w in ws]
+        for x, y, gr in zip(a, b, grads):
+            x.grad, y.grad = gr.clone(), gr.clone()
+        ours.step()
+        lib.step()
+    for x, y in zip(a, b):
+        torch.testing.assert_close(x.detach(), y.detach(), rtol=1e-12, atol=1e-14)
+
+
+# ---------------------------------------------------------------- grouping / shapes
+def test_grouping_first_appearance_order():
+    bufs = [torch.zeros(2, 4, 4), torch.zeros(1, 6, 4), torch.zeros(1, 4, 4), torch.zeros(1, 6, 4, dtype=torch.bfloat16)]
+    keys = list(group_blocks(bufs, bufs).keys())
+    assert [(k[1], k[2], k[3]) for k in keys] == [(torch.float32, 4, 4), (torch.float32, 6, 4), (torch.bfloat16, 6, 4)]
+    assert [i for i, _, _ in group_blocks(bufs, bufs)[keys[0]]] == [0, 2]
+
+
+MEMBENCH_COUNTS = [  # membench/scripts/monarch_benchmark/common.py:13-64
+    (12, 1024, 0, 163_603_456), (24, 1536, 0, 423_568_896), (24, 2048, 0, 690_587_648),
+    (28, 3072, 0, 1_564_388_352), (32, 4096, 11008, 2_970_882_048)]
+
+
+@pytest.mark.parametrize("layers,embd,inter,expected", MEMBENCH_COUNTS)
+def test_shape_rule_matches_reference_parameter_counts(layers, embd, inter, expected):
+    ps = shapes.llama_monarch_params(layers, embd, inter, 4)
+    assert sum(math.prod(s) for _, s in ps) == expected
+
+
+# ---------------------------------------------------------------- FP8 codec
+def test_e4m3_encoder_matches_torch_cast():
+    x = np.concatenate([np.linspace(-460, 460, 20001, dtype=np.float32),
+                        np.float32(2.0) ** np.arange(-12, 9, 0.125, dtype=np.float32),
+                        -np.float32(2.0) ** np.arange(-12, 9, 0.125, dtype=np.float32),
+                        np.array([0.0, -0.0, 2 ** -10, 3 * 2 ** -11], dtype=np.float32)])
+    clipped = np.clip(x, -448, 448)
+    ours = codec.e4m3_encode(x)
+    ref = torch.from_numpy(clipped).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(ours, ref)
+    np.testing.assert_array_equal(codec.e4m3_decode(ours),
+                                  torch.from_numpy(ref).view(torch.float8_e4m3fn).float().numpy())
+
+
+def _decades(n, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal(n) * np.logspace(-6, 1, n)).astype(np.float32)
+
+
+@pytest.mark.parametrize("signed", [True, False])
+def test_codec_round_trip_bound(signed):
+    x = _decades(1000 * 129, 9).reshape(1000, 129)      # tail group + 7 decades (test_coat_state_muon.py:27-28)
+    if not signed:
+        x = x * x
+    q, sc, ex, smm = codec.quantize(x, signed)
+    y = codec.dequantize(q, sc, ex, smm, signed).reshape(x.shape)
+    # The encoder stores q = 448 (|x|/absmax)^expand; e4m3 keeps q to a relative
+    # 2^-4 when normal (q >= 2^-6) and to an absolute 2^-10 when subnormal.  The
+    # decoder raises back to 1/expand, so |y/x - 1| <= 1 - (1 - eq)^(1/expand).
+    xf, yf = x.reshape(-1).astype(np.float64), y.reshape(-1).astype(np.float64)
+    groups = np.arange(xf.size) // 128
+    amax = np.maximum.reduceat(np.abs(xf), np.arange(0, xf.size, 128))[groups]
+    e = ex[groups].astype(np.float64)
+    q = 448.0 * (np.abs(xf) / amax) ** e
+    eq = np.maximum(2.0 ** -4, 2.0 ** -10 / np.maximum(q, 1e-300))
+    bound = np.maximum(1 - np.clip(1 - eq, 0, None) ** (1.0 / e), (1 + eq) ** (1.0 / e) - 1) + 1e-5
+    rel = np.abs(yf - xf) / np.maximum(np.abs(xf), 1e-300)
+    nz = xf != 0
+    assert np.all(rel[nz] <= bound[nz])
+    assert np.all(yf[~nz] == 0)
+    assert np.all(np.sign(y.reshape(-1)) == np.sign(x.reshape(-1)) * (y.reshape(-1) != 0)) or not signed
+
+
+def test_codec_special_groups():
+    const = np.full(128, 0.37, dtype=np.float32)
+    q, sc, ex, smm = codec.quantize(const, True)
+    assert ex[0] == 1.0                                    # ratio 1 -> expand = 1
+    np.testing.assert_allclose(codec.dequantize(q, sc, ex, smm, True), const, rtol=2 ** -4)
+    z = np.zeros(300, dtype=np.float32)
+    q, sc, ex, smm = codec.quantize(z, True)
+    assert np.all(q == 0) and np.all(codec.dequantize(q, sc, ex, smm, True) == 0)
+    # group of 2 decades: expand = floor(log2(448^2/2)/log2(100)*16)/16
+    x = np.array([1.0, 100.0] * 64, dtype=np.float32)
+    _, _, ex, smm = codec.quantize(x, False)
+    assert ex[0] == np.floor(np.log2(np.float32(100352.0)) / np.log2(np.float32(100.0)) * 16) / 16
+    assert smm[0] == np.float32(10.0)
+
+
+def test_codec_halving_invariant():
+    # test_coat_state_muon.py:40-51: dequantize, halve exactly, requantize gives the
+    # codes and metadata of quantizing the halved values directly
+    x = _decades(1000 * 129, 10)
+    for signed in (True, False):
+        v = x if signed else x * x
+        q, sc, ex, smm = codec.quantize(v, signed)
+        d = codec.dequantize(q, sc, ex, smm, signed)
+        a = codec.quantize(d * np.float32(0.5), signed)
+        b = codec.quantize((d * np.float32(0.5)).astype(np.float32), signed)
+        for u, w in zip(a, b):
+            np.testing.assert_array_equal(u, w)
+        # halving a group leaves its expansion unchanged and halves sqrt_minmax
+        np.testing.assert_array_equal(a[2], codec.quantize(d, signed)[2])
