@@ -63,9 +63,7 @@ int geometry(int rows, int cols, int ns_dtype, Geometry& g) {
   g.mp = int(mp);
   g.np_ = int(np_);
   g.nparts = std::max(mmuon::pack_nparts(g.mp, g.np_, g.transposed),
-                      ((int64_t(rows) * cols) % 128 == 0 && (!g.transposed || cols % 128 == 0))
-                          ? mmuon::fp8_pack_nparts(rows, cols, g.transposed)
-                          : 0);
+                      (int64_t(rows) * cols) % 128 == 0 ? mmuon::fp8_pack_nparts(rows, cols, g.transposed) : 0);
   return MMUON_OK;
 }
 
@@ -153,8 +151,6 @@ int mmuon_fp8_momentum_pack(const mmuon_group* g, float momentum, int32_t have_s
   if (g->fp8 == nullptr) return fail(MMUON_EINVAL, "null FP8 metadata table");
   if ((int64_t(g->rows) * g->cols) % 128 != 0)
     return fail(MMUON_EINVAL, "FP8 momentum needs rows*cols %% 128 == 0 (got %d x %d)", g->rows, g->cols);
-  if (geo.transposed && g->cols % 128 != 0)
-    return fail(MMUON_EINVAL, "FP8 momentum of tall blocks needs cols %% 128 == 0 (got %d)", g->cols);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int nparts = mmuon::fp8_pack_nparts(g->rows, g->cols, geo.transposed);
   mmuon::PackArgs a = pack_args(g, geo, momentum, nparts);

@@ -70,8 +70,10 @@ __device__ __forceinline__ float fp8_momentum_elem(const uint8_t* q, const Fp8Me
   return t + TG::load(g, i);
 }
 
-// rows <= cols: one wave per 128-group of a block (groups may wrap rows).
-template <class TG, class TX>
+// One wave per 128-group of a block (groups may wrap rows).  TRANS: the block
+// is tall (rows > cols) and X holds its transpose; the general fallback for
+// tall blocks whose width is not a multiple of 128 (scattered X stores).
+template <class TG, class TX, bool TRANS>
 __global__ __launch_bounds__(F8_NT) void fp8_pack_rows_kernel(PackArgs a, const mmuon_block_fp8* meta,
                                                               int rows, int cols, int have_state) {
   __shared__ float red[F8_NT / 64];
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(F8_NT) void fp8_pack_rows_kernel(PackArgs a, const 
       const float xv = TX::round(nv[h]);
       ss += xv * xv;
       const int64_t r = e / cols, c = e % cols;
-      TX::store(x, r * a.np + c, xv);
+      TX::store(x, TRANS ? c * a.np + r : r * a.np + c, xv);
     }
     uint8_t c0, c1;
     const Fp8Meta nm = fp8_quant_group(nv[0], nv[1], true, true, true, c0, c1);
@@ -182,7 +184,7 @@ __global__ __launch_bounds__(256) void zero_pads_kernel(void* xv, int m, int n, 
 }
 
 int fp8_pack_nparts(int rows, int cols, bool transposed) {
-  if (transposed) return ((rows + 63) / 64) * (cols / 128);
+  if (transposed && cols % 128 == 0) return ((rows + 63) / 64) * (cols / 128);
   const int64_t gpb = int64_t(rows) * cols / 128;
   return int((gpb + 3) / 4);
 }
@@ -198,12 +200,15 @@ int launch_fp8_pack(const PackArgs& a, const mmuon_block_fp8* meta, int rows, in
   }
 #define MMUON_F8_CASE(GD, XD, TG, TX)                                                          \
   if (grad_dtype == GD && x_dtype == XD) {                                                     \
-    if (transposed)                                                                            \
+    if (transposed && cols % 128 == 0)                                                         \
       hipLaunchKernelGGL((fp8_pack_cols_kernel<TG, TX>), grid, block, 0, s, a, meta, rows, cols, \
                          have_state);                                                          \
+    else if (transposed)                                                                       \
+      hipLaunchKernelGGL((fp8_pack_rows_kernel<TG, TX, true>), grid, block, 0, s, a, meta, rows, \
+                         cols, have_state);                                                    \
     else                                                                                       \
-      hipLaunchKernelGGL((fp8_pack_rows_kernel<TG, TX>), grid, block, 0, s, a, meta, rows, cols, \
-                         have_state);                                                          \
+      hipLaunchKernelGGL((fp8_pack_rows_kernel<TG, TX, false>), grid, block, 0, s, a, meta, rows, \
+                         cols, have_state);                                                    \
     return 0;                                                                                  \
   }
   MMUON_F8_CASE(MMUON_BF16, MMUON_BF16, BF16T, BF16T)

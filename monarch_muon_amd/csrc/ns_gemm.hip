@@ -12,11 +12,12 @@
 //
 // bf16 kernels: v_mfma_f32_32x32x16_bf16, fp32 accumulation, bf16 stage outputs.
 // 256-thread workgroups (4 waves) compute a 256x256 output tile; each wave a
-// 128x128 sub-tile (4x4 MFMA tiles, 256 accumulators).  K advances 64 at a
-// time through double-buffered LDS.  SYRK/POLY compute only the upper-triangle
-// tiles and write each tile and its mirror.  The X operand of PX is row-major
-// with the contraction along rows; it is staged into LDS as loaded and read
-// transposed with ds_read_b64_tr_b16.
+// 128x128 sub-tile (4x4 MFMA tiles, 256 accumulators in AGPRs).  K advances 32
+// at a time through a 4-slot LDS ring filled by direct global->LDS loads
+// (global_load_lds_dwordx4), three slices in flight ahead of the one in use.
+// SYRK/POLY compute only the upper-triangle tiles and write each tile and its
+// mirror.  The X operand of PX is row-major with the contraction along rows; it
+// is staged into LDS as loaded and read transposed with ds_read_b64_tr_b16.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -28,16 +29,14 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-constexpr int NT = 256;      // threads per workgroup
-constexpr int BK = 64;       // K tile
-constexpr int LDK = BK + 8;  // LDS row stride of K-contiguous tiles (144 B: conflict-free b128 reads)
-constexpr int XPAD = 32;     // LDS row padding of the row-major X tile (row stride = 64 mod 256 B)
-
-constexpr int BM = 256;      // output tile (both dims)
+constexpr int NT = 256;      // threads per workgroup (4 waves, 2 x 2)
+constexpr int BK = 32;       // K slice per pipeline stage
+constexpr int NSTAGE = 4;    // LDS ring depth (three slices in flight ahead of the one in use)
+constexpr int BM = 256;      // output tile, both dimensions
 constexpr int WM = 128;      // wave sub-tile
-constexpr int WN = 128;
-constexpr int TM = WM / 32;
-constexpr int TN = WN / 32;
+constexpr int TM = WM / 32;  // 32x32 MFMA tiles per wave and dimension
+constexpr int SLICE = 256 * BK;        // elements of one operand slice (16 KiB)
+constexpr int DMA_PER_OPERAND = SLICE * 2 / (NT * 16);  // 16-B direct loads per thread per slice
 
 // Workgroups are dispatched round-robin over the 8 XCDs.  Map workgroup w to
 // (block, tile) so that every tile of one block lands on the same XCD (and its
@@ -60,28 +59,6 @@ __device__ __forceinline__ void sym_tile(int t, int nt, int& ti, int& tj) {
   tj = i + t;
 }
 
-__device__ __forceinline__ bf16x8 lds_b128(const uint16_t* p) {
-  return *reinterpret_cast<const bf16x8*>(p);
-}
-
-// Transposed 8-element fragment of a row-major [k][col] LDS tile for a 32-wide
-// MFMA operand: lane l receives column (c0 + l%32), rows k0 + 8*(l/32) + [0,8).
-// ds_read_b64_tr_b16 works on groups of 16 lanes: lane i addresses 4 elements
-// of row i/4 at column 4*(i%4) of a 4x16 block and receives column i of it.
-__device__ __forceinline__ bf16x8 lds_tr_frag(const uint16_t* tile, int ld, int k0, int c0,
-                                              int lane) {
-  const int l16 = lane & 15;
-  const int krow = k0 + ((lane >> 5) << 3) + (l16 >> 2);
-  const int col = c0 + (((lane >> 4) & 1) << 4) + ((l16 & 3) << 2);
-  const uint16_t* p0 = tile + krow * ld + col;
-  const uint16_t* p1 = p0 + 4 * ld;
-  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0));
-  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p1));
-  typedef short i16x8 __attribute__((ext_vector_type(8)));
-  const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-  return __builtin_bit_cast(bf16x8, v);
-}
-
 __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
@@ -99,13 +76,214 @@ __device__ __forceinline__ void unpack4(uint2 r, float v[4]) {
   v[3] = __uint_as_float(r.y & 0xffff0000u);
 }
 
+// Wait until at most N direct-to-LDS loads of this thread are outstanding
+// (vector-memory loads complete in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 16-B direct global->LDS load: lane l of the wave lands at lds_base + 16*l
+// (M0 holds the wave-uniform LDS base).  Issued as inline assembly so that the
+// compiler's wait-count pass does not guard every later LDS read with a
+// vmcnt(0); the pipeline waits for exactly the slice it reads (wait_vm, in-order
+// completion of vector-memory loads) and then synchronises the workgroup.
+__device__ __forceinline__ void dma16(const uint16_t* g, uint16_t* lds_base) {
+  const uint32_t m0 = uint32_t(reinterpret_cast<uintptr_t>((lds_void*)lds_base));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(g), "s"(__builtin_amdgcn_readfirstlane(m0))
+               : "memory");
+}
+
+// Workgroup barrier that also stops the compiler from moving LDS reads above it.
+__device__ __forceinline__ void barrier() {
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// ----- LDS layouts --------------------------------------------------------
+// K-major slice [256 rows][32 k]: a row is four 16-B chunks; chunk c of row r
+// sits in slot c ^ ((r >> 2) & 3), so the 16 rows read by one quarter-wave's
+// ds_read_b128 cover all 64 banks.
+// Row-major X slice [32 k][256 cols]: a row is eight 64-B granules; granule g
+// of row k sits at g ^ (k & 3), so the four rows a ds_read_b64_tr_b16 group
+// touches land on distinct bank quarters.
+
+// Issue one K-major operand slice: 256 rows of 32 k starting at `src` (row
+// stride ld elements, k offset already applied).  Wave w, instruction q covers
+// rows 16*(4w+q) .. +15; lane l loads row l/4, chunk (l%4) ^ ((l>>4)&3).
+__device__ __forceinline__ void issue_kmajor(const uint16_t* src, int64_t ld, uint16_t* slice,
+                                             int wave, int lane) {
+  const int r_in = lane >> 2;
+  const int chunk = (lane & 3) ^ ((lane >> 4) & 3);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int grp = wave * 4 + q;
+    dma16(src + int64_t(grp * 16 + r_in) * ld + chunk * 8, slice + grp * 16 * BK);
+  }
+}
+
+// Issue one row-major X slice: 32 rows of 256 columns at `src` (row stride ld).
+// Wave w, instruction q covers rows 2*(4w+q) .. +1; lane l loads row l/32,
+// physical chunk l%32 = logical granule ((l%32)/4) ^ (row & 3), chunk l%4.
+__device__ __forceinline__ void issue_rowmajor(const uint16_t* src, int64_t ld, uint16_t* slice,
+                                               int wave, int lane) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int grp = wave * 4 + q;
+    const int row = grp * 2 + (lane >> 5);
+    const int lg = ((lane & 31) >> 2) ^ (row & 3);
+    dma16(src + int64_t(row) * ld + lg * 32 + (lane & 3) * 8, slice + grp * 2 * 256);
+  }
+}
+
+// 8-element K-major fragment of a 32-row MFMA operand (rows r0 + lane%32,
+// k = 16*kk + 8*(lane/32) + [0,8)).
+__device__ __forceinline__ bf16x8 frag_kmajor(const uint16_t* slice, int r0, int kk, int lane) {
+  const int r = r0 + (lane & 31);
+  const int c = (kk * 2 + (lane >> 5)) ^ ((r >> 2) & 3);
+  return *reinterpret_cast<const bf16x8*>(slice + r * BK + c * 8);
+}
+
+// Same fragment shape read transposed out of a row-major X slice: lane l
+// receives column c0 + l%32, rows 16*kk + 8*(l/32) + [0,8).  ds_read_b64_tr_b16
+// works on 16-lane groups: lane i addresses 4 elements of row i/4 at column
+// 4*(i%4) of a 4x16 block and receives column i of that block.
+__device__ __forceinline__ bf16x8 frag_rowmajor_tr(const uint16_t* slice, int c0, int kk, int lane) {
+  const int l16 = lane & 15;
+  const int col = c0 + (((lane >> 4) & 1) << 4) + ((l16 & 3) << 2);
+  const int gran = col >> 5, within = col & 31;
+  const int k0 = kk * 16 + ((lane >> 5) << 3) + (l16 >> 2);
+  const int k1 = k0 + 4;
+  const uint16_t* p0 = slice + k0 * 256 + ((gran ^ (k0 & 3)) << 5) + within;
+  const uint16_t* p1 = slice + k1 * 256 + ((gran ^ (k1 & 3)) << 5) + within;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p1));
+  typedef short i16x8 __attribute__((ext_vector_type(8)));
+  const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
 // ---------------------------------------------------------------------------
-// SYRK / POLY: symmetric m x m outputs, both operands K-contiguous rows.
+// The pipelined main loop shared by every stage.  ROWMAJOR_C: the column
+// operand is the row-major X stack (PX stages), else K-major (SYRK/POLY).
+// SWAP: D holds [col][row] (lane owns a row index and four consecutive column
+// indices) instead of [row][col].
+// ---------------------------------------------------------------------------
+// Ring slots are distinct LDS objects so that the compiler's wait-count pass
+// can tell the slices apart and wait only for the slice about to be read.
+struct Ring {
+  uint16_t* r0; uint16_t* r1; uint16_t* r2; uint16_t* r3;
+  uint16_t* c0; uint16_t* c1; uint16_t* c2; uint16_t* c3;
+  template <int S> __device__ __forceinline__ uint16_t* r() const {
+    if constexpr (S == 0) return r0; else if constexpr (S == 1) return r1;
+    else if constexpr (S == 2) return r2; else return r3;
+  }
+  template <int S> __device__ __forceinline__ uint16_t* c() const {
+    if constexpr (S == 0) return c0; else if constexpr (S == 1) return c1;
+    else if constexpr (S == 2) return c2; else return c3;
+  }
+};
+
+template <bool ROWMAJOR_C, bool SWAP>
+struct Pipe {
+  const uint16_t* rsrc;
+  int64_t rld;
+  const uint16_t* csrc;
+  int64_t cld;
+  int KT;
+  int wave, lane, wm, wn;
+
+  template <int S>
+  __device__ __forceinline__ void issue(const Ring& ring, int kt) const {
+    issue_kmajor(rsrc + kt * BK, rld, ring.template r<S>(), wave, lane);
+    if (ROWMAJOR_C) issue_rowmajor(csrc + int64_t(kt) * BK * cld, cld, ring.template c<S>(), wave, lane);
+    else issue_kmajor(csrc + kt * BK, cld, ring.template c<S>(), wave, lane);
+  }
+
+  template <int S>
+  __device__ __forceinline__ void compute(const Ring& ring, f32x16 (&acc)[TM][TM]) const {
+    const uint16_t* sr = ring.template r<S>();
+    const uint16_t* sc = ring.template c<S>();
+    // every fragment of the slice first (both 16-deep k steps), then the MFMAs
+    bf16x8 fr[BK / 16][TM], fc[BK / 16][TM];
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+#pragma unroll
+      for (int j = 0; j < TM; ++j)
+        fc[kk][j] = ROWMAJOR_C ? frag_rowmajor_tr(sc, wn * WM + j * 32, kk, lane)
+                               : frag_kmajor(sc, wn * WM + j * 32, kk, lane);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fr[kk][i] = frag_kmajor(sr, wm * WM + i * 32, kk, lane);
+    }
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+          acc[i][j] = SWAP ? mfma(fc[kk][j], fr[kk][i], acc[i][j]) : mfma(fr[kk][i], fc[kk][j], acc[i][j]);
+  }
+
+  // k-slice kt lives in ring slot S = kt % 4; slices kt+1, kt+2 are in flight.
+  template <int S>
+  __device__ __forceinline__ void step(const Ring& ring, int kt, f32x16 (&acc)[TM][TM]) const {
+    if (kt >= KT) return;
+    if (kt + 2 < KT) wait_vm<2 * 2 * DMA_PER_OPERAND>();
+    else if (kt + 1 < KT) wait_vm<2 * DMA_PER_OPERAND>();
+    else wait_vm<0>();
+    barrier();
+    if (kt + 3 < KT) issue<(S + 3) & 3>(ring, kt + 3);
+    compute<S>(ring, acc);
+  }
+
+  __device__ __forceinline__ void run(const Ring& ring, f32x16 (&acc)[TM][TM]) const {
+    issue<0>(ring, 0);
+    if (KT > 1) issue<1>(ring, 1);
+    if (KT > 2) issue<2>(ring, 2);
+    for (int kt = 0; kt < KT; kt += 4) {
+      step<0>(ring, kt, acc);
+      step<1>(ring, kt + 1, acc);
+      step<2>(ring, kt + 2, acc);
+      step<3>(ring, kt + 3, acc);
+    }
+  }
+};
+
+template <bool ROWMAJOR_C, bool SWAP>
+__device__ __forceinline__ void mainloop(const uint16_t* rsrc, int64_t rld, const uint16_t* csrc,
+                                         int64_t cld, int KT, const Ring& ring, f32x16 (&acc)[TM][TM]) {
+  Pipe<ROWMAJOR_C, SWAP> p;
+  p.rsrc = rsrc;
+  p.rld = rld;
+  p.csrc = csrc;
+  p.cld = cld;
+  p.KT = KT;
+  p.lane = threadIdx.x & 63;
+  p.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  p.wm = p.wave >> 1;
+  p.wn = p.wave & 1;
+  p.run(ring, acc);
+}
+
+#define MMUON_RING_DECL                                                                        \
+  __shared__ __attribute__((aligned(1024))) uint16_t r0_[SLICE], r1_[SLICE], r2_[SLICE], r3_[SLICE]; \
+  __shared__ __attribute__((aligned(1024))) uint16_t c0_[SLICE], c1_[SLICE], c2_[SLICE], c3_[SLICE]; \
+  Ring ring;                                                                                   \
+  ring.r0 = r0_; ring.r1 = r1_; ring.r2 = r2_; ring.r3 = r3_;                                  \
+  ring.c0 = c0_; ring.c1 = c1_; ring.c2 = c2_; ring.c3 = c3_;
+
+// ---------------------------------------------------------------------------
+// SYRK / POLY: symmetric m x m outputs, both operands K-major rows.
 // ---------------------------------------------------------------------------
 template <int STAGE>
 __global__ __launch_bounds__(NT, 1) void ns_sym_bf16(NsArgs a) {
-  constexpr int CPT = BM * (BK / 8) / NT;  // 16-B chunks per thread per operand
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][BM * LDK];
+  MMUON_RING_DECL
 
   const int nt = a.mp / BM;
   const int tiles = nt * (nt + 1) / 2;
@@ -115,7 +293,8 @@ __global__ __launch_bounds__(NT, 1) void ns_sym_bf16(NsArgs a) {
   sym_tile(t, nt, ti, tj);
 
   const uint16_t* src;
-  int ld, K;
+  int64_t ld;
+  int K;
   if (STAGE == NS_SYRK) {
     src = static_cast<const uint16_t*>(a.x_in) + int64_t(b) * a.mp * a.np;
     ld = a.np;
@@ -125,63 +304,16 @@ __global__ __launch_bounds__(NT, 1) void ns_sym_bf16(NsArgs a) {
     ld = a.mp;
     K = a.mp;
   }
-  const uint16_t* pa = src + int64_t(ti) * BM * ld;
-  const uint16_t* pb = src + int64_t(tj) * BM * ld;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  uint4 ra[CPT], rb[CPT];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int q = 0; q < CPT; ++q) {
-      const int c = tid + NT * q, row = c >> 3, kc = c & 7;
-      ra[q] = *reinterpret_cast<const uint4*>(pa + int64_t(row) * ld + k0 + kc * 8);
-      rb[q] = *reinterpret_cast<const uint4*>(pb + int64_t(row) * ld + k0 + kc * 8);
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int q = 0; q < CPT; ++q) {
-      const int c = tid + NT * q, row = c >> 3, kc = c & 7;
-      *reinterpret_cast<uint4*>(&lds[buf][0][row * LDK + kc * 8]) = ra[q];
-      *reinterpret_cast<uint4*>(&lds[buf][1][row * LDK + kc * 8]) = rb[q];
-    }
-  };
-
-  f32x16 acc[TM][TN];
+  f32x16 acc[TM][TM];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
-
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  const int KT = K / BK;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) gload((kt + 1) * BK);
-    const uint16_t* sA = lds[cur][0];
-    const uint16_t* sB = lds[cur][1];
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      bf16x8 fa[TM], fb[TN];
-      const int koff = kk * 16 + (lane >> 5) * 8;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) fa[i] = lds_b128(sA + (wm * WM + i * 32 + (lane & 31)) * LDK + koff);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) fb[j] = lds_b128(sB + (wn * WN + j * 32 + (lane & 31)) * LDK + koff);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma(fa[i], fb[j], acc[i][j]);
-    }
-    if (kt + 1 < KT) lstore(cur ^ 1);
-    __syncthreads();
-  }
+    for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
+  mainloop<false, false>(src + int64_t(ti) * BM * ld, ld, src + int64_t(tj) * BM * ld, ld, K / BK, ring, acc);
 
   // epilogue: D[i][j] in registers, lane holds column j and rows i..i+3.
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
   float s2 = 1.f;
   if (STAGE == NS_SYRK && a.scale != nullptr) {
     const float s = a.scale[b];
@@ -192,8 +324,8 @@ __global__ __launch_bounds__(NT, 1) void ns_sym_bf16(NsArgs a) {
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int col = tj * BM + wn * WN + j * 32 + (lane & 31);
+    for (int j = 0; j < TM; ++j) {
+      const int col = tj * BM + wn * WM + j * 32 + (lane & 31);
 #pragma unroll
       for (int qg = 0; qg < 4; ++qg) {
         const int row = ti * BM + wm * WM + i * 32 + qg * 8 + (lane >> 5) * 4;
@@ -231,14 +363,10 @@ __global__ __launch_bounds__(NT, 1) void ns_sym_bf16(NsArgs a) {
 //               parameter layout of tall blocks, param[j][i..i+3].
 // ---------------------------------------------------------------------------
 constexpr int PBN = 256;                     // output tile along n
-constexpr int LDX = PBN + XPAD;
 
 template <int STAGE, bool SWAP, class TP>
 __global__ __launch_bounds__(NT, 1) void ns_px_bf16(NsArgs a) {
-  constexpr int CPT_P = BM * (BK / 8) / NT;
-  constexpr int CPT_X = BK * (PBN / 8) / NT;
-  __shared__ __attribute__((aligned(16))) uint16_t sp[2][BM * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t sx[2][BK * LDX];
+  MMUON_RING_DECL
 
   const int tiles_j = a.np / PBN;
   const int tiles = (a.mp / BM) * tiles_j;
@@ -249,70 +377,16 @@ __global__ __launch_bounds__(NT, 1) void ns_px_bf16(NsArgs a) {
   const uint16_t* P = static_cast<const uint16_t*>(a.a_in) + int64_t(b) * a.mp * a.mp +
                       int64_t(ti) * BM * a.mp;
   const uint16_t* X = static_cast<const uint16_t*>(a.x_in) + int64_t(b) * a.mp * a.np;
-  const uint16_t* Xt = X + tj * PBN;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  uint4 rp[CPT_P], rx[CPT_X];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int q = 0; q < CPT_P; ++q) {
-      const int c = tid + NT * q, row = c >> 3, kc = c & 7;
-      rp[q] = *reinterpret_cast<const uint4*>(P + int64_t(row) * a.mp + k0 + kc * 8);
-    }
-#pragma unroll
-    for (int q = 0; q < CPT_X; ++q) {
-      const int c = tid + NT * q, row = c / (PBN / 8), cc = c % (PBN / 8);
-      rx[q] = *reinterpret_cast<const uint4*>(Xt + int64_t(k0 + row) * a.np + cc * 8);
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int q = 0; q < CPT_P; ++q) {
-      const int c = tid + NT * q, row = c >> 3, kc = c & 7;
-      *reinterpret_cast<uint4*>(&sp[buf][row * LDK + kc * 8]) = rp[q];
-    }
-#pragma unroll
-    for (int q = 0; q < CPT_X; ++q) {
-      const int c = tid + NT * q, row = c / (PBN / 8), cc = c % (PBN / 8);
-      *reinterpret_cast<uint4*>(&sx[buf][row * LDX + cc * 8]) = rx[q];
-    }
-  };
-
-  f32x16 acc[TM][TN];
+  f32x16 acc[TM][TM];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
+  mainloop<true, SWAP>(P, a.mp, X + tj * PBN, a.np, a.mp / BK, ring, acc);
 
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  const int KT = a.mp / BK;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < KT) gload((kt + 1) * BK);
-    const uint16_t* sP = sp[cur];
-    const uint16_t* sX = sx[cur];
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      bf16x8 fp[TM], fx[TN];
-      const int koff = kk * 16 + (lane >> 5) * 8;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) fp[i] = lds_b128(sP + (wm * WM + i * 32 + (lane & 31)) * LDK + koff);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) fx[j] = lds_tr_frag(sX, LDX, kk * 16, wn * WN + j * 32, lane);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = SWAP ? mfma(fx[j], fp[i], acc[i][j]) : mfma(fp[i], fx[j], acc[i][j]);
-    }
-    if (kt + 1 < KT) lstore(cur ^ 1);
-    __syncthreads();
-  }
-
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
   const float s = a.scale != nullptr ? a.scale[b] : 1.f;
   uint16_t* out = static_cast<uint16_t*>(a.out) + int64_t(b) * a.mp * a.np;
   typename TP::storage* prm = nullptr;
@@ -321,16 +395,16 @@ __global__ __launch_bounds__(NT, 1) void ns_px_bf16(NsArgs a) {
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
+    for (int j = 0; j < TM; ++j) {
 #pragma unroll
       for (int qg = 0; qg < 4; ++qg) {
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = acc[i][j][qg * 4 + e];
         if (SWAP) {
-          // lane: row i (X' row), columns jj..jj+3
+          // lane: row i (X' row), columns col..col+3
           const int row = ti * BM + wm * WM + i * 32 + (lane & 31);
-          const int col = tj * PBN + wn * WN + j * 32 + qg * 8 + (lane >> 5) * 4;
+          const int col = tj * PBN + wn * WM + j * 32 + qg * 8 + (lane >> 5) * 4;
           float xv[4];
           unpack4(*reinterpret_cast<const uint2*>(X + int64_t(row) * a.np + col), xv);
 #pragma unroll
@@ -348,8 +422,8 @@ __global__ __launch_bounds__(NT, 1) void ns_px_bf16(NsArgs a) {
             }
           }
         } else {
-          // lane: column j (X' column), rows ii..ii+3
-          const int col = tj * PBN + wn * WN + j * 32 + (lane & 31);
+          // lane: column j (X' column), rows row..row+3
+          const int col = tj * PBN + wn * WM + j * 32 + (lane & 31);
           const int row = ti * BM + wm * WM + i * 32 + qg * 8 + (lane >> 5) * 4;
 #pragma unroll
           for (int e = 0; e < 4; ++e) v[e] = s * fmaf(a.ca, bf2f(X[int64_t(row + e) * a.np + col]), v[e]);

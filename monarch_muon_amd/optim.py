@@ -319,10 +319,14 @@ class CoatStateMonarchMuon(MonarchMuonOptimizer):
         super().load_state_dict(state_dict)
         params = [p for group in self.param_groups for p in group["params"]]
         for key, dtypes in saved.items():
-            state = self.state[params[key]]
+            p = params[key]
+            state = self.state[p]
+            entry = state_dict["state"][key]
             for name, dtype in dtypes.items():
                 state[name] = state[name].to(dtype)
                 for meta in ("scale", "expand", "sqrt_minmax"):
                     mk = f"{meta}_{name}"
-                    if mk in state and state[mk].dtype != torch.float32:
-                        state[mk] = state[mk].to(torch.float32)
+                    if mk in entry:
+                        # the saved fp32 metadata itself (torch's cast to a bf16
+                        # parameter dtype would round it)
+                        state[mk] = entry[mk].detach().to(device=p.device, dtype=torch.float32).clone()
