@@ -10,16 +10,20 @@ namespace mmuon {
 
 // ---------------------------------------------------------------------------
 // bf16 <-> fp32.  bf16 is carried as its raw 16-bit pattern; conversion is
-// round-to-nearest-even with quiet-NaN preservation (the rounding torch uses
-// for every bf16 tensor op).
+// round-to-nearest-even (the rounding torch uses for every bf16 tensor op).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
 
+// gfx950 converts with v_cvt_pk_bf16_f32 (round to nearest even).
 __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
+// two floats -> packed bf16 pair (lo = a), one v_cvt_pk_bf16_f32
+__device__ __forceinline__ uint32_t f2bf2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // round a float to bf16 precision and back
