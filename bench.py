@@ -109,18 +109,20 @@ def instrumented_step(opt, lr=0.02):
 
 
 def kernel_symbol(kind, gl, it):
-    """The device-function family rocprof reports for a launch."""
+    """The kernel (template instance) rocprof reports for a launch, as it
+    appears in ``rocprofv3 --stats`` names (mmuon::(anonymous namespace)::...)."""
     if kind == "syrk":
         return "ns_sym_bf16<0>"
     if kind == "poly":
         return "ns_sym_bf16<1>"
     if kind == "px":
         if it < 4:
-            return "ns_px_bf16<2,true>"
-        return "ns_px_bf16<3,false>" if gl.transposed else "ns_px_bf16<3,true>"
+            return "ns_px_bf16<2, false, mmuon::BF16T>"
+        tp = "BF16T" if gl.struct.param_dtype == 1 else "F32T"
+        return f"ns_px_bf16<3, {'true' if gl.transposed else 'false'}, mmuon::{tp}>"
     if kind == "pack":
-        return "pack_cols" if gl.transposed else "pack_rows"
-    return kind
+        return "pack_cols_kernel" if gl.transposed else "pack_rows_kernel"
+    return kind + "_kernel"
 
 
 def stage_flops(kind, gl):
@@ -211,7 +213,16 @@ def main():
     ap.add_argument("--workload", default="6.89b-nb4")
     ap.add_argument("--instrumented", type=int, default=2, help="extra per-kernel-timed steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy (for HBM counter calibration)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        x = torch.ones(2 ** 28, dtype=torch.float32, device="cuda")
+        y = torch.empty_like(x)
+        y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": x.numel() * 4, "copy_bytes_written": y.numel() * 4}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the single-GPU optimizer step only; multi-GPU runs are not part of "
               "this build (see DESIGN.md for how the step would shard).", file=sys.stderr)

@@ -182,6 +182,7 @@ int ns_stage(const mmuon_group* g, const Geometry& geo, int it, int iters, int s
   a.cc = coeffs[2];
   a.alpha = alpha;
   a.transposed = geo.transposed ? 1 : 0;
+  a.vec = (g->flags & MMUON_GROUP_ALIGNED16) ? 1 : 0;
   void* cur = (it & 1) ? g->x1 : g->x0;
   void* nxt = (it & 1) ? g->x0 : g->x1;
   const float* sc = it == 0 ? g->scale : nullptr;

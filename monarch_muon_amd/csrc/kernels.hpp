@@ -40,6 +40,7 @@ struct NsArgs {
   float ca, cb, cc;   // quintic coefficients
   float alpha;        // apply: -lr * sqrt(rows / cols)
   int transposed;     // rows > cols
+  int vec;            // apply: every parameter block is 16-B aligned
 };
 
 // geometry helpers (tile sizes of the kernels)

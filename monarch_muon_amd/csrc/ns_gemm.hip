@@ -511,17 +511,41 @@ __global__ __launch_bounds__(NT, 1) void ns_sym_bf16(NsArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int PBN = 256;                     // output tile along n
 
+// param[o .. o+valid) += alpha * u (u = 8 bf16 in u8); one rounding to the
+// parameter dtype per element, as torch's foreach add with alpha.  `vec`:
+// 16-B aligned full chunk (8 bf16 = 16 B, 8 fp32 = 32 B).
 template <class TP>
 __device__ __forceinline__ void apply_chunk(typename TP::storage* prm, int64_t o, const uint4& u8, float alpha,
-                                            int valid) {
+                                            int valid, bool vec) {
   const uint32_t w[4] = {u8.x, u8.y, u8.z, u8.w};
+  float u[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    if (e < valid) {
-      const float u = __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
-      TP::store(prm, o + e, fmaf(alpha, u, TP::load(prm, o + e)));
+  for (int e = 0; e < 8; ++e) u[e] = __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+  if (vec && valid == 8) {
+    if constexpr (sizeof(typename TP::storage) == 2) {
+      uint4 pv = *reinterpret_cast<const uint4*>(prm + o);
+      uint32_t pw[4] = {pv.x, pv.y, pv.z, pv.w};
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float p0 = __uint_as_float(pw[h] << 16), p1 = __uint_as_float(pw[h] & 0xffff0000u);
+        pw[h] = f2bf2(fmaf(alpha, u[2 * h], p0), fmaf(alpha, u[2 * h + 1], p1));
+      }
+      *reinterpret_cast<uint4*>(prm + o) = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+    } else {
+      float4* q = reinterpret_cast<float4*>(prm + o);
+      float4 a0 = q[0], a1 = q[1];
+      a0.x = fmaf(alpha, u[0], a0.x); a0.y = fmaf(alpha, u[1], a0.y);
+      a0.z = fmaf(alpha, u[2], a0.z); a0.w = fmaf(alpha, u[3], a0.w);
+      a1.x = fmaf(alpha, u[4], a1.x); a1.y = fmaf(alpha, u[5], a1.y);
+      a1.z = fmaf(alpha, u[6], a1.z); a1.w = fmaf(alpha, u[7], a1.w);
+      q[0] = a0;
+      q[1] = a1;
     }
+    return;
   }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (e < valid) TP::store(prm, o + e, fmaf(alpha, u[e], TP::load(prm, o + e)));
 }
 
 template <int STAGE, bool TRANS, class TP>
@@ -578,6 +602,8 @@ __global__ __launch_bounds__(NT, 1) void ns_px_bf16(NsArgs a) {
   // or (n x m) for a tall block
   auto* prm = reinterpret_cast<typename TP::storage*>(a.blocks[b].param);
   const float alpha = a.alpha;
+  // 16-B vector access: aligned blocks and a row length that keeps chunks aligned
+  const bool vec = a.vec && ((TRANS ? a.m : a.n) % 8 == 0);
   if (TRANS) {
     const int tid = threadIdx.x;
     const int c = (tid & 31) * 8;
@@ -586,13 +612,13 @@ __global__ __launch_bounds__(NT, 1) void ns_px_bf16(NsArgs a) {
       const int pr = c0 + r, pc = r0 + c;
       if (pr >= a.n || pc >= a.m) continue;
       const uint4 u8 = *reinterpret_cast<const uint4*>(tile + tile_off(r, c));
-      apply_chunk<TP>(prm, int64_t(pr) * a.m + pc, u8, alpha, min(8, a.m - pc));
+      apply_chunk<TP>(prm, int64_t(pr) * a.m + pc, u8, alpha, min(8, a.m - pc), vec);
     }
   } else {
     const int m = a.m, n = a.n;
     tile_cols(tile, [&](int i, int j, const uint4& v) {
       const int pr = r0 + i, pc = c0 + j;
-      if (pr < m && pc < n) apply_chunk<TP>(prm, int64_t(pr) * n + pc, v, alpha, min(8, n - pc));
+      if (pr < m && pc < n) apply_chunk<TP>(prm, int64_t(pr) * n + pc, v, alpha, min(8, n - pc), vec);
     });
   }
 }
