@@ -117,9 +117,9 @@ def kernel_symbol(kind, gl, it):
         return "ns_sym_bf16<1>"
     if kind == "px":
         if it < 4:
-            return "ns_px_bf16<2, false, mmuon::BF16T>"
+            return "ns_px_bf16<2, false, BF16T>"
         tp = "BF16T" if gl.struct.param_dtype == 1 else "F32T"
-        return f"ns_px_bf16<3, {'true' if gl.transposed else 'false'}, mmuon::{tp}>"
+        return f"ns_px_bf16<3, {'true' if gl.transposed else 'false'}, {tp}>"
     if kind == "pack":
         return "pack_cols_kernel" if gl.transposed else "pack_rows_kernel"
     return kind + "_kernel"
@@ -158,6 +158,18 @@ def stage_exec_flops(kind, gl):
 def pack_bytes(gl, momentum_bytes, grad_bytes=2, x_bytes=2):
     lay = gl.ws.layout
     return gl.nblocks * lay.m * lay.n * (grad_bytes + 2 * momentum_bytes + x_bytes)
+
+
+def hbm_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (FETCH_SIZE and WRITE_SIZE, each scaled by a plain copy's reading);
+    None when no summary covers this workload and kernel."""
+    path = ROOT / "profiles" / f"hbm_traffic_{workload}.json"
+    try:
+        data = json.loads(path.read_text())
+        return round(data["kernels"][kernel]["bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 # ---------------------------------------------------------------- CPU baseline
@@ -270,6 +282,7 @@ def main():
     d_ms, d_n, d_fl, d_ex = per[dominant]
     d_avg = d_ms / d_n
     achieved = (d_fl / d_n) / (d_avg * 1e-3) / 1e12
+    traffic = hbm_traffic(w.name, dominant)
     kernels = {k: {"avg_ms": round(v[0] / v[1], 4), "launches_per_step": v[1] // reps,
                    "ms_per_step": round(v[0] / reps, 3),
                    **({"alg_tflops": round(v[2] / (v[0] * 1e-3) / 1e12, 1),
@@ -293,7 +306,7 @@ def main():
         "median_event_ms": round(median_ms, 3),
         "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "avg_launch_ms": round(d_avg, 4),
+                     "traffic": traffic, "avg_launch_ms": round(d_avg, 4),
                      "alg_flops_per_launch": d_fl / d_n, "exec_tflops": round((d_ex / d_n) / (d_avg * 1e-3) / 1e12, 1)},
         "newton_schulz": {"ms": round(ns_ms, 3), "alg_tflop": round(ns_flops(w) / 1e12, 2),
                           "alg_tflops": round(ns_tf, 1), "frac_peak": round(ns_tf / PEAK_BF16_TFLOPS, 4)},
