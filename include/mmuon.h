@@ -59,14 +59,16 @@ typedef struct mmuon_block_fp8 {
   float* sqrt_minmax;
 } mmuon_block_fp8;
 
-/* Workspace geometry of one same-shape group, from mmuon_ns_layout(). */
+/* Workspace geometry of one same-shape group, from mmuon_ns_layout().
+   Matrix layout inside the stacks: fp32 row-major; bf16 in 32-column panels,
+   element (i, j) of an R-row matrix at (j / 32) * R * 32 + i * 32 + j % 32. */
 typedef struct mmuon_ns_layout_t {
   int32_t m, n;        /* Newton-Schulz orientation: m = min(r,c), n = max(r,c) */
   int32_t mp, np_;     /* padded m, n (multiples of the kernels' tiles)          */
   int32_t nparts;      /* partial sums of squares per block                      */
   int32_t ns_dtype;    /* MMUON_BF16 or MMUON_F32                                */
-  int64_t x_bytes;     /* one X stack  [N][mp][np_]                               */
-  int64_t a_bytes;     /* one Gram stack [N][mp][mp]                              */
+  int64_t x_bytes;     /* one X stack  [N] x (mp x np_)                           */
+  int64_t a_bytes;     /* one Gram stack [N] x (mp x mp)                          */
   int64_t part_bytes;  /* partial sums   [N][nparts] fp32                         */
 } mmuon_ns_layout_t;
 
@@ -115,7 +117,7 @@ int mmuon_fp8_momentum_pack(const mmuon_group* g, float momentum, int32_t have_s
                             void* stream);
 
 /* Newton-Schulz over the group's stack (already packed into g->x0) followed by
-   the weight update:
+   the weight update (X ping-pongs between x0 and x1):
      X <- X / (||X||_F + 1e-7)  (norm from the packed partial sums)
      repeat iters: A = X X^T ; P = b A + c A A ; X = a X + P X
      param <- param + alpha * cast(X) (un-transposed), alpha = -lr*sqrt(r/c)

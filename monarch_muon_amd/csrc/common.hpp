@@ -29,18 +29,40 @@ __device__ __forceinline__ uint32_t f2bf2(float a, float b) {
 // round a float to bf16 precision and back
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
+// ---------------------------------------------------------------------------
+// Newton-Schulz workspace layout.  bf16 stacks (X, Gram, polynomial) are kept
+// in 32-column panels: element (i, j) of a matrix with R rows sits at
+//   (j / 32) * (R * 32) + i * 32 + j % 32,
+// so the 32-wide K slice of 256 rows that an MFMA stage loads is one contiguous
+// 16 KiB run.  fp32 stacks are plain row-major [R][cols].
+// ---------------------------------------------------------------------------
+constexpr int PANEL = 32;
+
+__host__ __device__ __forceinline__ int64_t panel_off(int64_t rows, int64_t i, int64_t j) {
+  return (j >> 5) * (rows << 5) + (i << 5) + (j & 31);
+}
+
 // Element access by storage type tag.
+// xoff(mp, np, i, j): offset of X-stack element (i, j) within one block.
 struct F32T {
   using storage = float;
   static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
   static __device__ __forceinline__ void store(float* p, int64_t i, float v) { p[i] = v; }
   static __device__ __forceinline__ float round(float v) { return v; }
+  static __device__ __forceinline__ int64_t xoff(int mp, int np, int64_t i, int64_t j) {
+    (void)mp;
+    return i * np + j;
+  }
 };
 struct BF16T {
   using storage = uint16_t;
   static __device__ __forceinline__ float load(const uint16_t* p, int64_t i) { return bf2f(p[i]); }
   static __device__ __forceinline__ void store(uint16_t* p, int64_t i, float v) { p[i] = f2bf(v); }
   static __device__ __forceinline__ float round(float v) { return rbf(v); }
+  static __device__ __forceinline__ int64_t xoff(int mp, int np, int64_t i, int64_t j) {
+    (void)np;
+    return panel_off(mp, i, j);
+  }
 };
 
 // ---------------------------------------------------------------------------

@@ -98,7 +98,7 @@ __global__ __launch_bounds__(F8_NT) void fp8_pack_rows_kernel(PackArgs a, const 
       const float xv = TX::round(nv[h]);
       ss += xv * xv;
       const int64_t r = e / cols, c = e % cols;
-      TX::store(x, TRANS ? c * a.np + r : r * a.np + c, xv);
+      TX::store(x, TRANS ? TX::xoff(a.mp, a.np, c, r) : TX::xoff(a.mp, a.np, r, c), xv);
     }
     uint8_t c0, c1;
     const Fp8Meta nm = fp8_quant_group(nv[0], nv[1], true, true, true, c0, c1);
@@ -164,7 +164,7 @@ __global__ __launch_bounds__(F8_NT) void fp8_pack_cols_kernel(PackArgs a, const 
       const int rl = half + k, r = r0 + rl;
       const float v = tile[rl][cl];
       ss += v * v;
-      if (r < a.np) TX::store(x, int64_t(c0 + cl) * a.np + r, v);
+      if (r < a.np) TX::store(x, TX::xoff(a.mp, a.np, c0 + cl, r), v);
     }
   }
   const float tot = block_sum<F8_NT>(ss, red);
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void zero_pads_kernel(void* xv, int m, int n, 
   const int64_t total = int64_t(mp) * np_;
   for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
     const int i = int(e / np_), j = int(e % np_);
-    if (i >= m || j >= n) TX::store(x, e, 0.f);
+    if (i >= m || j >= n) TX::store(x, TX::xoff(mp, np_, i, j), 0.f);
   }
 }
 

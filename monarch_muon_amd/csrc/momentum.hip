@@ -61,22 +61,37 @@ constexpr int PACK_ITERS = 4;
 constexpr int PACK_ELEMS = PACK_NT * 8 * PACK_ITERS;  // X elements per workgroup (row layout)
 constexpr int PACK_TILE = 64;                          // transposed layout: 64 x 64 tiles
 
-// rows <= cols: X[b][i][j] = buf[b][i][j]; the X stack is walked linearly.
+// rows <= cols: X[b][i][j] = buf[b][i][j], 8 elements per thread.
+// fp32 X: the padded [mp][np] extent is walked in row-major order.
+// bf16 X (32-column panels; mp, np multiples of 256): a workgroup owns 32 rows x
+// 256 columns, and per iteration a wave covers 8 rows x 64 columns, so every
+// wave reads whole 128-B lines of the momentum and gradient rows and writes two
+// contiguous 512-B panel runs.
 template <class TG, class TB, class TX>
 __global__ __launch_bounds__(PACK_NT) void pack_rows_kernel(PackArgs a) {
   __shared__ float red[PACK_NT / 64];
+  constexpr bool PANELS = sizeof(typename TX::storage) == 2;
   const int b = blockIdx.y;
   const mmuon_block_ref ref = a.blocks[b];
   const auto* g = reinterpret_cast<const typename TG::storage*>(ref.grad);
   auto* buf = reinterpret_cast<typename TB::storage*>(ref.buf);
   auto* x = reinterpret_cast<typename TX::storage*>(a.x) + int64_t(b) * a.mp * a.np;
   const int64_t total = int64_t(a.mp) * a.np;
+  const int tiles_j = a.np / 256;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float ss = 0.f;
 #pragma unroll
   for (int it = 0; it < PACK_ITERS; ++it) {
-    const int64_t e = int64_t(blockIdx.x) * PACK_ELEMS + (int64_t(it) * PACK_NT + threadIdx.x) * 8;
-    if (e >= total) break;
-    const int i = int(e / a.np), j = int(e % a.np);
+    int i, j;
+    if constexpr (PANELS) {
+      i = (blockIdx.x / tiles_j) * 32 + wave * 8 + (lane >> 3);
+      j = (blockIdx.x % tiles_j) * 256 + it * 64 + (lane & 7) * 8;
+    } else {
+      const int64_t e = int64_t(blockIdx.x) * PACK_ELEMS + (int64_t(it) * PACK_NT + threadIdx.x) * 8;
+      if (e >= total) break;
+      i = int(e / a.np);
+      j = int(e % a.np);
+    }
     float v[8];
     if (a.vec && i < a.m && j + 8 <= a.n) {
       const int64_t s = int64_t(i) * a.n + j;
@@ -102,7 +117,7 @@ __global__ __launch_bounds__(PACK_NT) void pack_rows_kernel(PackArgs a) {
     }
 #pragma unroll
     for (int q = 0; q < 8; ++q) ss += v[q] * v[q];
-    Vec8<TX>::store(x + e, v);
+    Vec8<TX>::store(x + TX::xoff(a.mp, a.np, i, j), v);  // 8 elements stay in one panel
   }
   const float tot = block_sum<PACK_NT>(ss, red);
   if (threadIdx.x == 0) a.partial[int64_t(b) * a.nparts + blockIdx.x] = tot;
@@ -165,7 +180,7 @@ __global__ __launch_bounds__(PACK_NT) void pack_cols_kernel(PackArgs a) {
         v[q] = tile[seg + h * 8 + q][ir];
         ss += v[q] * v[q];
       }
-      Vec8<TX>::store(x + int64_t(i0 + ir) * a.np + j0 + seg + h * 8, v);
+      Vec8<TX>::store(x + TX::xoff(a.mp, a.np, i0 + ir, j0 + seg + h * 8), v);
     }
   }
   const float tot = block_sum<PACK_NT>(ss, red);

@@ -64,9 +64,14 @@ class Workspace:
                    torch.empty(nblocks, dtype=torch.float32, device=device))
 
     def x_view(self, which: int, dtype: torch.dtype, nblocks: int) -> torch.Tensor:
-        """The X stack ``[N, mp, np]`` (``which`` = 0 or 1) as a typed view."""
-        t = self.x0 if which == 0 else self.x1
-        return t.view(dtype).view(nblocks, self.layout.mp, self.layout.np_)
+        """The X stack (``which`` = 0 or 1) as ``[N, mp, np]``.  fp32 stacks are
+        row-major (a view); bf16 stacks are stored in 32-column panels
+        (``[N][np/32][mp][32]``) and come back as a row-major copy."""
+        t = (self.x0 if which == 0 else self.x1).view(dtype)
+        mp, np_ = self.layout.mp, self.layout.np_
+        if dtype == torch.float32:
+            return t.view(nblocks, mp, np_)
+        return t.view(nblocks, np_ // 32, mp, 32).permute(0, 2, 1, 3).reshape(nblocks, mp, np_)
 
 
 @dataclass
