@@ -11,15 +11,17 @@
 // 1 afterwards.
 //
 // bf16 kernels: v_mfma_f32_32x32x16_bf16, fp32 accumulation, bf16 stage outputs.
-// 256-thread workgroups (4 waves) compute a 256x256 output tile; each wave a
-// 128x128 sub-tile (4x4 MFMA tiles, 256 accumulators in AGPRs).  K advances 32
-// at a time through a 4-slot LDS ring filled by direct global->LDS loads
-// (global_load_lds_dwordx4), three slices in flight ahead of the one in use.
-// SYRK/POLY compute only the upper-triangle tiles and write each tile and its
-// mirror.  Every bf16 stack is stored in 32-column panels (panel_off), so a K
-// slice is contiguous in HBM.  The X operand of PX has the contraction along its
-// rows; its slice is staged into LDS as stored and read transposed with
-// ds_read_b64_tr_b16.
+// 256-thread workgroups (4 waves) compute a 256x128 output tile; each wave a
+// 128x64 sub-tile (4x2 MFMA tiles, 128 accumulators).  Two workgroups share a
+// CU (72 KiB of LDS and at most 256 registers per wave each), so one
+// workgroup's epilogue and memory waits overlap the other's MFMAs.  K advances
+// 32 at a time through a 3-slot LDS ring filled by direct global->LDS loads
+// (global_load_lds_dwordx4), one slice in flight ahead of the one in use.
+// SYRK/POLY compute only the tiles on or above the diagonal blocks and write
+// each off-diagonal tile and its mirror.  Every bf16 stack is stored in
+// 32-column panels (panel_off), so a K slice is contiguous in HBM.  The X
+// operand of PX has the contraction along its rows; its slice is staged into LDS
+// as stored and read transposed with ds_read_b64_tr_b16.
 #include <algorithm>
 #include <atomic>
 
@@ -34,82 +36,68 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-constexpr int NT = 256;      // threads per workgroup (4 waves, 2 x 2)
-constexpr int BK = 32;       // K slice per pipeline stage (one panel)
-constexpr int NSTAGE = 4;    // LDS ring depth (three slices in flight ahead of the one in use)
-constexpr int BM = 256;      // output tile, both dimensions
-constexpr int WM = 128;      // wave sub-tile
-constexpr int TM = WM / 32;  // 32x32 MFMA tiles per wave and dimension
-constexpr int SLICE = 256 * BK;          // elements of one operand slice (16 KiB)
-constexpr int SLOT = 2 * SLICE;          // elements of one ring slot: row + column slice (32 KiB)
-// Epilogue staging: half an output tile (128 x 256 bf16, 64 KiB) in ring slot 3
-// and the 32 KiB above the ring, so ring slots 0..2 can take the next tile's
-// first slices while the current tile is stored.
-constexpr int STAGE_OFF = 3 * SLOT;      // elements
-constexpr int LDS_ELEMS = STAGE_OFF + 128 * 256;  // 160 KiB
+constexpr int NT = 512;       // threads per workgroup (8 waves, 2 x 4)
+constexpr int WG_PER_CU = 1;  // workgroups resident per CU
+constexpr int BK = 32;        // K slice per pipeline stage (one panel)
+constexpr int NSTAGE = 4;     // LDS ring depth: NSTAGE-2 slices in flight behind the next one
+constexpr int BM = 256;       // output tile rows
+constexpr int BN = 256;       // output tile columns
+constexpr int WM = 128;       // wave sub-tile rows
+constexpr int WN = 64;        // wave sub-tile columns
+constexpr int NWN = BN / WN;  // waves along the columns
+constexpr int NWAVES = NT / 64;
+constexpr int TMI = WM / 32;  // 32x32 MFMA tiles per wave: 4 x 2
+constexpr int TMJ = WN / 32;
+constexpr int RSLICE = BM * BK;           // elements of a row-operand slice (16 KiB)
+constexpr int CSLICE = BN * BK;           // elements of a column-operand slice
+constexpr int SLOT = RSLICE + CSLICE;     // one ring slot
+constexpr int LDS_ELEMS = NSTAGE * SLOT;
+constexpr int RDMA = RSLICE * 2 / (NT * 16);  // 16-B direct loads per thread per row slice
+constexpr int CDMA = CSLICE * 2 / (NT * 16);  // ... per column slice
+constexpr int SLICE_DMA = RDMA + CDMA;
+static_assert((BM / WM) * NWN == NWAVES, "waves tile the workgroup tile");
+static_assert(LDS_ELEMS >= BN * 256, "the staged tile fits in the ring");
 
-// Persistent workgroups: workgroup w takes virtual tiles w, w + G, w + 2G, ...
-// (G = gridDim.x, a multiple of 8).  Workgroups are dispatched round-robin over
-// the 8 XCDs, so virtual tile v runs on XCD v % 8; decode_tile maps v to
+// Workgroups are dispatched round-robin over the 8 XCDs, and a workgroup takes
+// virtual tiles w, w + G, w + 2G, ... (G = gridDim.x, a multiple of 8, every
+// workgroup resident), so virtual tile w runs on XCD w % 8.  Map w to
 // (block, tile) so that every tile of one block lands on the same XCD (and its
-// L2) and the tiles of a block are taken back to back.
-__device__ __forceinline__ bool decode_tile(int v, int tiles, int N, int& b, int& t) {
-  const int xcd = v & 7, local = v >> 3;
+// L2), and the tiles of a block run in the same round: they start together and
+// stream the block's panels in step, which the L2 serves.
+__device__ __forceinline__ bool decode_tile(int w, int tiles, int N, int& b, int& t) {
+  const int xcd = w & 7, local = w >> 3;
   b = xcd + 8 * (local / tiles);
   t = local % tiles;
   return b < N;
 }
 
-// First virtual tile >= v (stepping by the grid) whose block exists, or `total`.
-__device__ __forceinline__ int next_tile(int v, int total, int tiles, int N, int& b, int& t) {
-  for (; v < total; v += gridDim.x)
-    if (decode_tile(v, tiles, N, b, t)) return v;
-  return total;
-}
-
-__device__ __forceinline__ void sym_tile(int t, int nt, int& ti, int& tj) {
+// Tiles of a symmetric m x m product: BM-row band ti, BN-column band tc with
+// tc >= R ti, R = BM / BN (the upper triangle and the diagonal blocks), ti-major.
+constexpr int R_SYM = BM / BN;
+__device__ __forceinline__ void sym_tile(int t, int nc, int& ti, int& tc) {
   int i = 0;
-  while (t >= nt - i) {
-    t -= nt - i;
+  while (t >= nc - R_SYM * i) {
+    t -= nc - R_SYM * i;
     ++i;
   }
   ti = i;
-  tj = i + t;
-}
-
-// Wave-uniform scalar load of one float (SMEM path: it is not counted by vmcnt,
-// so it never waits on the direct-to-LDS loads in flight).
-__device__ __forceinline__ float sload_f32(const float* p) {
-  float v;
-  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
-  return v;
+  tc = R_SYM * i + t;
 }
 
 __device__ __forceinline__ f32x16 mfma(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// threadIdx.x through an opaque move: per-lane epilogue addresses derived from
-// it are recomputed in every tile instead of being hoisted out of the tile loop
-// (where they would stay live across the main loop and spill).
-__device__ __forceinline__ int fresh_tid() {
-  int t;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(t) : "v"(int(threadIdx.x)));
-  return t;
-}
-
-// Wait until at most n vector-memory instructions of this thread are
-// outstanding (they complete in issue order).  n is wave-uniform and rounded
-// down to a multiple of 8 (63 at most, the counter's range), which only waits
-// longer.
-__device__ __forceinline__ void wait_vm(int n) {
-  if (n >= 63) asm volatile("s_waitcnt vmcnt(63)" ::: "memory");
-  else if (n >= 48) asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
-  else if (n >= 40) asm volatile("s_waitcnt vmcnt(40)" ::: "memory");
-  else if (n >= 32) asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
-  else if (n >= 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-  else if (n >= 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+// Wait until at most N vector-memory instructions of this thread are
+// outstanding (they complete in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N == 0 || N == 4 || N == 6 || N == 8 || N == 12, "unsupported wait count");
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+  else if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -139,36 +127,38 @@ __device__ __forceinline__ void barrier() {
 }
 
 // ----- LDS layouts --------------------------------------------------------
-// K-major slice [256 rows][32 k] (256 rows of one panel): a row is four 16-B
-// chunks; chunk c of row r sits in slot c ^ ((r >> 2) & 3), so the 16 rows read
-// by one quarter-wave's ds_read_b128 cover all 64 banks.
-// X slice of a PX stage [8 panels][32 k][32 columns]: 64-B rows as in HBM; the
+// K-major slice [rows][32 k] (consecutive rows of one panel): a row is four
+// 16-B chunks; chunk c of row r sits in slot c ^ ((r >> 2) & 3), so the 16 rows
+// read by one quarter-wave's ds_read_b128 cover all 64 banks.
+// X slice of a PX stage [BN/32 panels][32 k][32 columns]: 64-B rows as in HBM; the
 // 4 rows x 64 B a half-wave's ds_read_b64_tr_b16 touches are 256 contiguous
 // bytes, one access per bank.
 
-// Issue one K-major operand slice: 256 consecutive panel rows at `src`, one
-// contiguous 16 KiB run.  Wave w, instruction q covers rows 16*(4w+q) .. +15
-// (1 KiB); lane l loads row l/4, chunk (l%4) ^ ((l>>4)&3) (kmajor_lane_offset).
+// Issue one K-major operand slice of 16*4*Q rows at `src` (one contiguous run
+// of the panel).  Wave w, instruction q covers rows 16*(Q*w+q) .. +15 (1 KiB);
+// lane l loads row l/4, chunk (l%4) ^ ((l>>4)&3) (kmajor_lane_offset).
 __device__ __forceinline__ uint32_t kmajor_lane_offset(int lane) {
   const int chunk = (lane & 3) ^ ((lane >> 4) & 3);
   return uint32_t(((lane >> 2) * PANEL + chunk * 8) * 2);
 }
+template <int Q>
 __device__ __forceinline__ void issue_kmajor(const uint16_t* src, uint32_t loff, uint32_t slice, int wave) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int grp = wave * 4 + q;
+  for (int q = 0; q < Q; ++q) {
+    const int grp = wave * Q + q;
     dma16(src + grp * 16 * PANEL, loff, slice + grp * 1024);
   }
 }
 
-// Issue one X slice of a PX stage: rows k0 .. k0+31 of the 8 column panels at
-// src, src + pstride, ... (2 KiB contiguous each).  Wave w, instruction q covers
-// panel (4w+q)/2, rows 16*((4w+q)%2) .. +15; the lane offset is 16*l bytes.
+// Issue one X slice of a PX stage: rows k0 .. k0+31 of the BN/32 column panels
+// at src, src + pstride, ... (2 KiB contiguous each).  Wave w, instruction q
+// covers panel g/2, rows 16*(g%2) .. +15 with g = CDMA*w + q; the lane offset
+// is 16*l bytes.
 __device__ __forceinline__ void issue_xslice(const uint16_t* src, int64_t pstride, uint32_t loff,
                                              uint32_t slice, int wave) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int grp = wave * 4 + q;
+  for (int q = 0; q < CDMA; ++q) {
+    const int grp = wave * CDMA + q;
     dma16(src + (grp >> 1) * pstride + (grp & 1) * 16 * PANEL, loff, slice + grp * 1024);
   }
 }
@@ -214,12 +204,12 @@ __device__ __forceinline__ bf16x8 frag_rowmajor_tr(const uint16_t* slice, uint32
 // ---------------------------------------------------------------------------
 // MFMA operand fragments of one 16-deep k step held by one wave.
 struct Frags {
-  bf16x8 r[TM];
-  bf16x8 c[TM];
+  bf16x8 r[TMI];
+  bf16x8 c[TMJ];
 };
 
-// Identity fragments: IDENT = 1 adds v*I on the row-operand side (acc += v X
-// over the K slice that crosses the tile's diagonal rows), IDENT = 2 on the
+// Identity fragments: IDENT_ROW adds v*I on the row-operand side (acc += v X
+// over the K slices that cross the tile's diagonal rows), IDENT_COL on the
 // column-operand side (acc += v A).  v is split into two bf16 parts (hi + lo)
 // so the identity term keeps ~16 bits; the products are exact and accumulate
 // in fp32 with the rest of the dot product.
@@ -238,215 +228,227 @@ __device__ __forceinline__ bf16x8 ident_frag(float v, int kk, int lane) {
 
 template <bool ROWMAJOR_C, int IDENT = IDENT_NONE>
 struct Pipe {
-  // per tile
   const uint16_t* rsrc;  // row operand: panel 0, first row of the tile
   const uint16_t* csrc;  // column operand: panel 0, first row (K-major) / first panel (X)
-  int diag0;             // K index of this wave's first identity row / column
-  // per launch
-  int64_t pstride;       // elements per panel of the row operand (rows * 32)
-  int64_t cstride;       // elements per panel of the column operand
+  int64_t pstride;       // elements per panel (rows * 32)
   int KT;
   int wave, lane, wm, wn;
   uint16_t* lds;  // ring slot s at lds + s*SLOT: row-operand slice, then column-operand slice
   uint32_t lds0;  // LDS byte address of lds
   uint32_t r_loff, c_loff;        // per-lane DMA byte offsets
   uint32_t kfrag[BK / 16];        // per-lane K-major fragment bases
-  uint32_t tfrag[TM];             // per-lane transposed fragment bases (one per column tile)
+  uint32_t tfrag[TMJ];            // per-lane transposed fragment bases (one per column tile)
+  int diag0;                      // K index of this wave's first identity row / column
   float id_hi, id_lo;             // identity scalar split into two bf16 parts
 
-  __device__ __forceinline__ void init(int64_t pstride_, int64_t cstride_, int KT_, uint16_t* lds_,
-                                       float ident_v) {
-    pstride = pstride_;
-    cstride = cstride_;
-    KT = KT_;
-    lane = threadIdx.x & 63;
-    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    wm = wave >> 1;
-    wn = wave & 1;
-    lds = lds_;
-    lds0 = lds_addr(lds_);
-    r_loff = kmajor_lane_offset(lane);
-    c_loff = ROWMAJOR_C ? uint32_t(lane * 16) : r_loff;
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) kfrag[kk] = kmajor_frag_base(kk, lane);
-#pragma unroll
-    for (int j = 0; j < TM; ++j) tfrag[j] = rowmajor_frag_base(wn * (WM / 32) + j, lane);
-    id_hi = rbf(ident_v);
-    id_lo = ident_v - id_hi;
+  __device__ __forceinline__ uint16_t* rslot(int kt) const { return lds + (kt % NSTAGE) * SLOT; }
+
+  // Slice src_kt into the ring slot of slice slot_kt.
+  __device__ __forceinline__ void issue(int src_kt, int slot_kt) const {
+    const uint32_t rs = lds0 + (slot_kt % NSTAGE) * SLOT * 2;
+    const uint32_t cs = rs + RSLICE * 2;
+    issue_kmajor<RDMA>(rsrc + src_kt * pstride, r_loff, rs, wave);
+    if (ROWMAJOR_C) issue_xslice(csrc + src_kt * BK * PANEL, pstride, c_loff, cs, wave);
+    else issue_kmajor<CDMA>(csrc + src_kt * pstride, r_loff, cs, wave);
   }
 
-  // rsrc_ / csrc_: panel-layout operands at the tile's first row (first panel
-  // for the X operand of PX); diag: K index of the tile's first row (IDENT_ROW)
-  // or column (IDENT_COL).
-  __device__ __forceinline__ void set_tile(const uint16_t* rsrc_, const uint16_t* csrc_, int diag) {
-    rsrc = rsrc_;
-    csrc = csrc_;
-    diag0 = diag + (IDENT == IDENT_ROW ? wm : wn) * WM;
+  // Direct load q (0 .. RDMA+CDMA-1) of slice `src_kt` into the ring slot of
+  // slice `slot_kt` (the same slice, except for the harmless refill of a
+  // consumed slot at the end of the loop).
+  template <int Q>
+  __device__ __forceinline__ void issue_one(int src_kt, int slot_kt) const {
+    const uint32_t rs = lds0 + (slot_kt % NSTAGE) * SLOT * 2;
+    if constexpr (Q < RDMA) {
+      const int grp = wave * RDMA + Q;
+      dma16(rsrc + src_kt * pstride + grp * 16 * PANEL, r_loff, rs + grp * 1024);
+    } else {
+      const int grp = wave * CDMA + (Q - RDMA);
+      const uint32_t cs = rs + RSLICE * 2 + grp * 1024;
+      if (ROWMAJOR_C)
+        dma16(csrc + src_kt * BK * PANEL + (grp >> 1) * pstride + (grp & 1) * 16 * PANEL, c_loff, cs);
+      else
+        dma16(csrc + src_kt * pstride + grp * 16 * PANEL, r_loff, cs);
+    }
   }
 
-  __device__ __forceinline__ uint16_t* rslot(int kt) const { return lds + (kt & (NSTAGE - 1)) * SLOT; }
-  __device__ __forceinline__ uint16_t* cslot(int kt) const { return rslot(kt) + SLICE; }
-
-  __device__ __forceinline__ void issue(int kt) const {
-    const uint32_t rs = lds0 + (kt & (NSTAGE - 1)) * SLOT * 2;
-    const uint32_t cs = rs + SLICE * 2;
-    issue_kmajor(rsrc + kt * pstride, r_loff, rs, wave);
-    if (ROWMAJOR_C) issue_xslice(csrc + kt * BK * PANEL, cstride, c_loff, cs, wave);
-    else issue_kmajor(csrc + kt * cstride, r_loff, cs, wave);
-  }
-
-  // Slices 0..2 of the tile into ring slots 0..2 (slot 3 stays free for the
-  // epilogue staging).  Slice 0 is issued before the previous tile's epilogue
-  // stores, slices 1 and 2 after them, so only the wait for slice 0 has to
-  // allow for the stores.
-  __device__ __forceinline__ void prologue_first() const { issue(0); }
-  __device__ __forceinline__ void prologue_rest() const {
-    if (KT > 1) issue(1);
-    if (KT > 2) issue(2);
-  }
-
-  // Fragment reads of k step kk (0 or 1) of slice kt.
+  // Fragment reads of k step KK (0 or 1) of slice kt.
   template <int KK>
   __device__ __forceinline__ void load(int kt, Frags& f) const {
     const uint16_t* sr = rslot(kt);
-    const uint16_t* sc = cslot(kt);
+    const uint16_t* sc = sr + RSLICE;
 #pragma unroll
-    for (int j = 0; j < TM; ++j)
-      f.c[j] = ROWMAJOR_C ? frag_rowmajor_tr(sc, tfrag[j], KK) : frag_kmajor(sc, kfrag[KK], wn * WM + j * 32);
+    for (int j = 0; j < TMJ; ++j)
+      f.c[j] = ROWMAJOR_C ? frag_rowmajor_tr(sc, tfrag[j], KK) : frag_kmajor(sc, kfrag[KK], wn * WN + j * 32);
 #pragma unroll
-    for (int i = 0; i < TM; ++i) f.r[i] = frag_kmajor(sr, kfrag[KK], wm * WM + i * 32);
+    for (int i = 0; i < TMI; ++i) f.r[i] = frag_kmajor(sr, kfrag[KK], wm * WM + i * 32);
   }
 
-  // F >= 0: this slice crosses the identity at fragment F (32 rows/columns);
-  // the identity fragments of k step KK are built on the spot.
+  // Identity MFMAs of k step KK when this slice crosses the identity at
+  // fragment F (32 rows/columns); the identity fragments are built on the spot.
   template <int KK, int F>
-  __device__ __forceinline__ void math(const Frags& f, f32x16 (&acc)[TM][TM]) const {
+  __device__ __forceinline__ void ident(const Frags& f, f32x16 (&acc)[TMI][TMJ]) const {
+    const bf16x8 ih = ident_frag(id_hi, KK, lane), il = ident_frag(id_lo, KK, lane);
+    if constexpr (IDENT == IDENT_ROW) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+      for (int j = 0; j < TMJ; ++j) {
+        acc[F][j] = mfma(ih, f.c[j], acc[F][j]);
+        acc[F][j] = mfma(il, f.c[j], acc[F][j]);
+      }
+    } else {
 #pragma unroll
-      for (int j = 0; j < TM; ++j) acc[i][j] = mfma(f.r[i], f.c[j], acc[i][j]);
-    if constexpr (F >= 0) {
-      const bf16x8 ih = ident_frag(id_hi, KK, lane), il = ident_frag(id_lo, KK, lane);
-      if constexpr (IDENT == IDENT_ROW) {
-#pragma unroll
-        for (int j = 0; j < TM; ++j) {
-          acc[F][j] = mfma(ih, f.c[j], acc[F][j]);
-          acc[F][j] = mfma(il, f.c[j], acc[F][j]);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          acc[i][F] = mfma(f.r[i], ih, acc[i][F]);
-          acc[i][F] = mfma(f.r[i], il, acc[i][F]);
-        }
+      for (int i = 0; i < TMI; ++i) {
+        acc[i][F] = mfma(f.r[i], ih, acc[i][F]);
+        acc[i][F] = mfma(f.r[i], il, acc[i][F]);
       }
     }
+  }
+
+  template <int KK, int F>
+  __device__ __forceinline__ void math(const Frags& f, f32x16 (&acc)[TMI][TMJ]) const {
+#pragma unroll
+    for (int i = 0; i < TMI; ++i)
+#pragma unroll
+      for (int j = 0; j < TMJ; ++j) acc[i][j] = mfma(f.r[i], f.c[j], acc[i][j]);
+    if constexpr (F >= 0) ident<KK, F>(f, acc);
   }
 
   // Fragments ping-pong at half-slice granularity: the k step 1 reads of slice kt
   // stream in under the k step 0 MFMAs, and (after the slice-kt+1 barrier) the
   // k step 0 reads of slice kt+1 under the k step 1 MFMAs.  At the barrier of
-  // step kt every wave has consumed slice kt-1, so its slot takes slice kt+3.
-  // Step kt waits for slice kt+1, with slice kt+2 allowed in flight.
+  // step kt every wave has consumed slice kt-1, so its slot takes slice
+  // kt+NSTAGE-1; those direct loads are interleaved one by one with the k step 1
+  // MFMAs so the memory pipeline drains while the matrix cores stay busy.
   template <int F>
-  __device__ __forceinline__ void step(int kt, Frags& fa, Frags& fb, f32x16 (&acc)[TM][TM]) const {
+  __device__ __forceinline__ void body(int kt, Frags& fa, Frags& fb, f32x16 (&acc)[TMI][TMJ]) const {
     load<1>(kt, fb);
     math<0, F>(fa, acc);
-    if (kt + 1 < KT) {
-      if (kt + 2 < KT) wait_vm(8);
-      else wait_vm(0);
-      barrier();
-      if (kt + 3 < KT) issue(kt + 3);
-    }
-    // unconditional so the wait counts before the second MFMA half only cover
-    // fb: on the last step this reads a stale slot whose values are never used
+    wait_vm<(NSTAGE - 3) * SLICE_DMA>();  // slice kt+1; the later ones may stay in flight
+    barrier();
+    // on the last step this reads a slot whose values are never used
     load<0>(kt + 1, fa);
-    math<1, F>(fb, acc);
+    // slice kt+NSTAGE-1; near the end a consumed slot is refilled with slice KT-1
+    // instead, so every step has the same shape
+    const int src = kt + NSTAGE - 1 < KT ? kt + NSTAGE - 1 : KT - 1;
+    const int slot = kt + NSTAGE - 1;
+#define MMUON_MFMA_DMA(g)                                                            \
+    acc[(g) / TMJ][(g) % TMJ] = mfma(fb.r[(g) / TMJ], fb.c[(g) % TMJ], acc[(g) / TMJ][(g) % TMJ]); \
+    if constexpr ((g) < SLICE_DMA) issue_one<(g)>(src, slot);                      \
+    __builtin_amdgcn_sched_barrier(0);
+    MMUON_MFMA_DMA(0) MMUON_MFMA_DMA(1) MMUON_MFMA_DMA(2) MMUON_MFMA_DMA(3)
+    MMUON_MFMA_DMA(4) MMUON_MFMA_DMA(5) MMUON_MFMA_DMA(6) MMUON_MFMA_DMA(7)
+#undef MMUON_MFMA_DMA
+    static_assert(TMI * TMJ == 8 && SLICE_DMA <= 8, "one direct load per MFMA of the k step");
+    if constexpr (F >= 0) ident<1, F>(fb, acc);
   }
 
-  // The tile's main loop, after prologue_first() and prologue_rest().  extra:
-  // vector-memory instructions this thread issued between the two (the previous
-  // tile's epilogue stores); they complete in order behind slice 0.
-  __device__ __forceinline__ void run(f32x16 (&acc)[TM][TM], int extra) const {
+  __device__ __forceinline__ void run(f32x16 (&acc)[TMI][TMJ]) const {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TMI; ++i)
 #pragma unroll
-      for (int j = 0; j < TM; ++j) acc[i][j] = f32x16{};
-    // slice 0 visible; the stores and slices 1 and 2 may remain in flight
-    wait_vm(8 * (KT > 2 ? 2 : KT - 1) + extra);
+      for (int j = 0; j < TMJ; ++j) acc[i][j] = f32x16{};
+    // slices 0 .. NSTAGE-2 (beyond the last slice: refills with slice KT-1)
+#pragma unroll
+    for (int q = 0; q < NSTAGE - 1; ++q) issue(q < KT ? q : KT - 1, q);
+    wait_vm<(NSTAGE - 2) * SLICE_DMA>();  // slice 0 visible, the others may stay in flight
     barrier();
     Frags fa, fb;
     load<0>(0, fa);
     if constexpr (IDENT == IDENT_NONE) {
-      for (int kt = 0; kt < KT; ++kt) step<-1>(kt, fa, fb, acc);
+      for (int kt = 0; kt < KT; ++kt) body<-1>(kt, fa, fb, acc);
     } else {
-      // the four 32-deep slices starting at diag0 cross this wave's identity
-      // fragments 0..3 in order (diag0 is a multiple of 128)
+      // the slices starting at diag0 cross this wave's identity fragments in
+      // order (diag0 is a multiple of the wave's extent along K)
+      constexpr int NI = IDENT == IDENT_ROW ? TMI : TMJ;
       const int kd = diag0 / BK;
-      int kt = 0;
-      for (; kt < kd; ++kt) step<-1>(kt, fa, fb, acc);
-      step<0>(kt, fa, fb, acc);
-      step<1>(kt + 1, fa, fb, acc);
-      step<2>(kt + 2, fa, fb, acc);
-      step<3>(kt + 3, fa, fb, acc);
-      for (kt += 4; kt < KT; ++kt) step<-1>(kt, fa, fb, acc);
+      for (int kt = 0; kt < kd; ++kt) body<-1>(kt, fa, fb, acc);
+      body<0>(kd, fa, fb, acc);
+      body<1>(kd + 1, fa, fb, acc);
+      if constexpr (NI == 4) {
+        body<2>(kd + 2, fa, fb, acc);
+        body<3>(kd + 3, fa, fb, acc);
+      }
+      for (int kt = kd + NI; kt < KT; ++kt) body<-1>(kt, fa, fb, acc);
     }
+    wait_vm<0>();  // the refills of the last two steps land before the ring is reused
   }
 };
 
+// rsrc / csrc: panel-layout operands at the tile's first row (first panel for
+// the X operand of PX); pstride: elements per panel.  ident_v: the identity
+// scalar; diag: K index of the tile's first row (IDENT_ROW) or column (IDENT_COL).
+template <bool ROWMAJOR_C, int IDENT = IDENT_NONE>
+__device__ __forceinline__ void mainloop(const uint16_t* rsrc, const uint16_t* csrc, int64_t pstride,
+                                         int KT, uint16_t* lds, f32x16 (&acc)[TMI][TMJ],
+                                         float ident_v = 0.f, int diag = 0) {
+  Pipe<ROWMAJOR_C, IDENT> p;
+  p.rsrc = rsrc;
+  p.csrc = csrc;
+  p.pstride = pstride;
+  p.KT = KT;
+  p.lane = threadIdx.x & 63;
+  p.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  p.wm = p.wave / NWN;
+  p.wn = p.wave % NWN;
+  p.lds = lds;
+  p.lds0 = lds_addr(lds);
+  p.r_loff = kmajor_lane_offset(p.lane);
+  p.c_loff = ROWMAJOR_C ? uint32_t(p.lane * 16) : p.r_loff;
+#pragma unroll
+  for (int kk = 0; kk < BK / 16; ++kk) p.kfrag[kk] = kmajor_frag_base(kk, p.lane);
+#pragma unroll
+  for (int j = 0; j < TMJ; ++j) p.tfrag[j] = rowmajor_frag_base(p.wn * TMJ + j, p.lane);
+  p.diag0 = diag + (IDENT == IDENT_ROW ? p.wm * WM : p.wn * WN);
+  p.id_hi = rbf(ident_v);
+  p.id_lo = ident_v - p.id_hi;
+  p.run(acc);
+}
+
 // ---------------------------------------------------------------------------
-// Output staging.  T[j][i] = D[i][j] (the accumulator tile, lane-major in j) is
-// staged in LDS half at a time (T rows 128h .. 128h+127, 64 KiB) so that every
-// global store is a 16-B chunk of a contiguous 1 KiB run.  Staged row r is 512 B
-// of 32 16-B chunks; chunk c sits at c ^ g(r), g(r) = 4 (r & 3) + ((r >> 2) & 3).
-// That keeps three access patterns free of bank conflicts: the accumulator
-// writes (16 consecutive rows, one chunk), the row reads of stage_rows (4 rows x
-// 4 chunks) and the transposed reads of stage_cols (4 rows x 2 chunks).
+// Output staging.  After the main loop the LDS ring is idle; the tile is staged
+// there as T[j][i] = D[i][j] (BN rows j of 512 B) so that every global store
+// is a 16-B chunk of a contiguous 1 KiB run.  Chunk c of row r sits at c ^ g(r),
+// g(r) = 4 (r & 3) + ((r >> 2) & 3).  That keeps three access patterns free of
+// bank conflicts: the accumulator writes (16 consecutive rows, one chunk), the
+// row reads of stage_rows (4 rows x 4 chunks) and the transposed reads of
+// stage_cols (4 rows x 2 chunks).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t tile_off(int r, int c) {
   const int g = ((r & 3) << 2) | ((r >> 2) & 3);
   return uint32_t(r * 512 + ((((c >> 3) ^ g)) << 4) | ((c & 7) << 1));
 }
 
-// Lane geometry of the D[i][j] accumulator layout of one wave: lane holds
-// column j = wn*128 + 32*tj + lane%32 and rows i = wm*128 + 32*ti + 8*qg + 4*(lane/32) + e.
-struct Lane {
-  int lane, wm, wn;
-  __device__ __forceinline__ int col(int tj) const { return wn * WM + tj * 32 + (lane & 31); }
-  __device__ __forceinline__ int row(int ti, int qg) const { return wm * WM + ti * 32 + qg * 8 + (lane >> 5) * 4; }
-};
-
-// Half h of T (rows j = 128h + r) into the staging area: the two waves with
-// wn == h own those columns of D.  f scales every value before the bf16 rounding.
-__device__ __forceinline__ void stage_half(char* stage, const f32x16 (&acc)[TM][TM], const Lane& L, float f) {
+// D[i][j] accumulators of this wave -> T[j][i] in the staging area, each value
+// scaled by f before the bf16 rounding.  Lane geometry: the lane holds column
+// j = 64 wn + 32 tj + lane%32 and rows i = 128 wm + 32 ti + 8 qg + 4 (lane/32) + e.
+__device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI][TMJ], float f) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / NWN, wn = wave % NWN;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+  for (int i = 0; i < TMI; ++i) {
 #pragma unroll
-    for (int j = 0; j < TM; ++j) {
+    for (int j = 0; j < TMJ; ++j) {
 #pragma unroll
       for (int qg = 0; qg < 4; ++qg) {
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = f * acc[i][j][qg * 4 + e];
-        *reinterpret_cast<uint2*>(stage + tile_off(j * 32 + (L.lane & 31), L.row(i, qg))) =
-            make_uint2(f2bf2(v[0], v[1]), f2bf2(v[2], v[3]));
+        const int row = wn * WN + j * 32 + (lane & 31);
+        const int col = wm * WM + i * 32 + qg * 8 + (lane >> 5) * 4;
+        *reinterpret_cast<uint2*>(stage + tile_off(row, col)) = make_uint2(f2bf2(v[0], v[1]), f2bf2(v[2], v[3]));
       }
-      // one 32x32 block at a time: keeps the accumulator reads from being
-      // hoisted (and their values held in VGPRs) across the whole tile
-      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
 
 // Staged rows -> a panel-layout destination with the same rows: dst[r][i] =
-// S[r][i] for the 128 staged rows, dst at the first staged row of the tile's
-// first column panel.  One wave instruction writes rows 16u .. 16u+15 of one
-// panel (1 KiB contiguous); 16 stores per thread.
-__device__ __forceinline__ void stage_rows(const char* stage, uint16_t* dst, int64_t pstride, int tid) {
-  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+// T[r][i] for the BN staged rows, dst at the first staged row of the tile's
+// first column panel (panel stride pstride).  One wave instruction writes rows
+// 16u .. 16u+15 of one panel (1 KiB contiguous).
+__device__ __forceinline__ void stage_rows(const char* stage, uint16_t* dst, int64_t pstride) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll 4
-  for (int it = 0; it < 16; ++it) {
-    const int u = wave + 4 * it;  // 8 panels x 8 row blocks
+  for (int it = 0; it < 8 * (BN / 16) / NWAVES; ++it) {
+    const int u = wave + NWAVES * it;  // 8 panels x BN/16 row blocks
     const int q = u & 7, r = (u >> 3) * 16 + (lane >> 2);
     const int i = q * 32 + (lane & 3) * 8;
     const uint4 v = *reinterpret_cast<const uint4*>(stage + tile_off(r, i));
@@ -454,20 +456,19 @@ __device__ __forceinline__ void stage_rows(const char* stage, uint16_t* dst, int
   }
 }
 
-// Staged columns -> rows of the destination: dst[i][r] = S[r][i] (256 rows i,
-// 128 columns r).  ds_read_b64_tr_b16 (16-lane groups): lane l of a group
-// addresses S row r0 + l/4 at column i0 + 4*(l%4) and receives S[r0..r0+3][i0 + l];
+// Staged columns -> rows of the destination: dst[i][r] = T[r][i] (256 rows i,
+// BN columns r).  ds_read_b64_tr_b16 (16-lane groups): lane l of a group
+// addresses T row r0 + l/4 at column i0 + 4*(l%4) and receives T[r0..r0+3][i0 + l];
 // two reads give 8 consecutive r of destination row i0 + l.  The four groups of
 // a wave take consecutive 8-column chunks, so one wave instruction covers
 // destination rows i0 .. i0+15, columns 32t .. 32t+31: one panel's contiguous
-// 1 KiB.  `fn(i, r, uint4)` consumes destination row i, columns r..r+7; 16
-// calls per thread.
+// 1 KiB.  `fn(i, r, uint4)` consumes destination row i, columns r..r+7.
 template <class Fn>
-__device__ __forceinline__ void stage_cols(const char* stage, int tid, Fn&& fn) {
-  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+__device__ __forceinline__ void stage_cols(const char* stage, Fn&& fn) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, grp = lane >> 4;
 #pragma unroll 2
-  for (int task = wave; task < 64; task += 4) {
+  for (int task = wave; task < 16 * (BN / 32); task += NWAVES) {
     const int i0 = (task & 15) * 16, r0 = (task >> 4) * 32 + grp * 8;
     const int tr = r0 + (l16 >> 2), tc = i0 + ((l16 & 3) << 2);
     const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(stage + tile_off(tr, tc)));
@@ -482,88 +483,76 @@ __device__ __forceinline__ void stage_cols(const char* stage, int tid, Fn&& fn) 
 }
 
 // ---------------------------------------------------------------------------
-// SYRK / POLY: symmetric m x m outputs, both operands K-major rows.  Persistent:
-// after a tile's main loop the next tile's first three slices are issued before
-// the tile is stored, so their latency and the stores overlap.
+// SYRK / POLY: symmetric m x m outputs, both operands K-major rows.  A tile is
+// a 256-row band ti x 128-column band tc with tc >= 2 ti; the two tiles that
+// cover a diagonal 256 x 256 block write it directly, every other tile writes
+// itself and its mirror.
 // ---------------------------------------------------------------------------
 template <int STAGE>
-__global__ __launch_bounds__(NT, 1) void ns_sym_bf16(NsArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint16_t lds[LDS_ELEMS];
-  char* stage = reinterpret_cast<char*>(lds + STAGE_OFF);
-
-  const int nt = a.mp / BM;
-  const int tiles = nt * (nt + 1) / 2;
-  const int total = 8 * ((a.N + 7) / 8) * tiles;
-  const int K = STAGE == NS_SYRK ? a.kx : a.mp;
-  const int64_t pstride = int64_t(a.mp) * PANEL;
-  const uint16_t* base = static_cast<const uint16_t*>(STAGE == NS_SYRK ? a.x_in : a.a_in);
-  const int64_t bstride = int64_t(a.mp) * (STAGE == NS_SYRK ? a.np : a.mp);
-  const int wn = (threadIdx.x >> 6) & 1;
-
-  // POLY: acc = A A + (b/c) A, so P = c acc = b A + c A A
-  Pipe<false, STAGE == NS_POLY ? IDENT_COL : IDENT_NONE> p;
-  p.init(pstride, pstride, K / BK, lds, STAGE == NS_POLY ? a.cb / a.cc : 0.f);
-
+__device__ __forceinline__ void sym_work(const NsArgs& a, uint16_t* lds, int v) {
+  const int nt = a.mp / BM, nc = a.mp / BN;
+  const int tiles = nt * nc - R_SYM * nt * (nt - 1) / 2;
   int b, t;
-  int v = next_tile(blockIdx.x, total, tiles, a.N, b, t);
-  if (v >= total) return;
-  int ti, tj;
-  sym_tile(t, nt, ti, tj);
-  p.set_tile(base + b * bstride + ti * BM * PANEL, base + b * bstride + tj * BM * PANEL, tj * BM);
-  p.prologue_first();
-  p.prologue_rest();
-  int extra = 0;
-  f32x16 acc[TM][TM];
-  while (true) {
-    p.run(acc, extra);
-    barrier();  // every wave is done with the ring
-    const int cb = b, cti = ti, ctj = tj;
-    v = next_tile(v + gridDim.x, total, tiles, a.N, b, t);
-    if (v < total) {
-      sym_tile(t, nt, ti, tj);
-      p.set_tile(base + b * bstride + ti * BM * PANEL, base + b * bstride + tj * BM * PANEL, tj * BM);
-      p.prologue_first();
-    }
-    // epilogue: T[j][i] = C[r0 + i][c0 + j]; T's rows are the mirror tile
-    // C[c0 + j][r0 + i] (the only write on the diagonal), its columns the direct tile.
-    const int tid = fresh_tid();
-    const Lane L{tid & 63, (tid >> 6) >> 1, (tid >> 6) & 1};
-    float f = STAGE == NS_POLY ? a.cc : 1.f;  // SYRK: s^2 on the first iteration
-    if (STAGE == NS_SYRK && a.scale != nullptr) {
-      const float sc = sload_f32(a.scale + cb);
-      f = sc * sc;
-    }
-    uint16_t* out = static_cast<uint16_t*>(a.out) + cb * int64_t(a.mp) * a.mp;
-    const int r0 = cti * BM, c0 = ctj * BM;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (wn == h) stage_half(stage, acc, L, f);
-      barrier();
-      stage_rows(stage, out + (r0 / PANEL) * pstride + int64_t(c0 + 128 * h) * PANEL, pstride, tid);
-      if (cti != ctj) {
-        uint16_t* dst = out + ((c0 + 128 * h) / PANEL) * pstride + int64_t(r0) * PANEL;
-        stage_cols(stage, tid, [&](int i, int r, const uint4& u) {
-          *reinterpret_cast<uint4*>(dst + (r >> 5) * pstride + i * PANEL + (r & 31)) = u;
-        });
-      }
-      if (h == 0) barrier();  // half 1 overwrites the staging area
-    }
-    if (v >= total) break;
-    p.prologue_rest();
-    extra = cti != ctj ? 64 : 32;  // stores per thread issued after slice 0
+  if (!decode_tile(v, tiles, a.N, b, t)) return;
+  int ti, tc;
+  sym_tile(t, nc, ti, tc);
+
+  const uint16_t* src;
+  int K;
+  if (STAGE == NS_SYRK) {
+    src = static_cast<const uint16_t*>(a.x_in) + int64_t(b) * a.mp * a.np;
+    K = a.kx;
+  } else {
+    src = static_cast<const uint16_t*>(a.a_in) + int64_t(b) * a.mp * a.mp;
+    K = a.mp;
+  }
+  const int64_t pstride = int64_t(a.mp) * PANEL;
+  const int r0 = ti * BM, c0 = tc * BN;
+  f32x16 acc[TMI][TMJ];
+  if (STAGE == NS_SYRK)
+    mainloop<false>(src + r0 * PANEL, src + c0 * PANEL, pstride, K / BK, lds, acc);
+  else  // acc = A A + (b/c) A, so P = c acc = b A + c A A
+    mainloop<false, IDENT_COL>(src + r0 * PANEL, src + c0 * PANEL, pstride, K / BK, lds, acc, a.cb / a.cc, c0);
+
+  float f = STAGE == NS_POLY ? a.cc : 1.f;  // SYRK: s^2 on the first iteration
+  if (STAGE == NS_SYRK && a.scale != nullptr) {
+    const float s = a.scale[b];
+    f = s * s;
+  }
+  uint16_t* out = static_cast<uint16_t*>(a.out) + int64_t(b) * a.mp * a.mp;
+  char* stage = reinterpret_cast<char*>(lds);
+  barrier();  // every wave is done with the ring
+  stage_tile(stage, acc, f);
+  barrier();
+  const bool diag = tc < R_SYM * (ti + 1);  // the tile meets a diagonal BM x BM block
+  // direct tile C[r0 + i][c0 + r] = T[r][i] (a square diagonal tile is written
+  // once, through its mirror)
+  if (R_SYM > 1 || !diag) {
+    uint16_t* dst = out + (c0 / PANEL) * pstride + int64_t(r0) * PANEL;
+    stage_cols(stage, [&](int i, int r, const uint4& u) {
+      *reinterpret_cast<uint4*>(dst + (r >> 5) * pstride + i * PANEL + (r & 31)) = u;
+    });
+  }
+  // mirror C[c0 + r][r0 + i] = T[r][i]
+  if (R_SYM == 1 || !diag) stage_rows(stage, out + (r0 / PANEL) * pstride + int64_t(c0) * PANEL, pstride);
+}
+
+template <int STAGE>
+__global__ __launch_bounds__(NT, WG_PER_CU) void ns_sym_bf16(NsArgs a, int total) {
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[LDS_ELEMS];
+  for (int v = blockIdx.x; v < total; v += gridDim.x) {
+    sym_work<STAGE>(a, lds, v);
+    barrier();  // the staging area is read before the next tile's loads refill the ring
   }
 }
 
 // ---------------------------------------------------------------------------
-// PX / PX_APPLY: X' = s (a X + P X), m x n output tile (256 x 256), K = m.
+// PX / PX_APPLY: X' = s (a X + P X), m x n output tile (256 x 128), K = m.
 // D[i][j] in registers (lane holds column j, rows i..i+3); the a X term enters
 // the accumulation as (a I) X.  T[j][i] = X'[r0 + i][c0 + j] is staged in LDS;
 // X' rows (PX, and the parameter rows of an untransposed block) are T's
 // columns, the parameter rows of a tall block (param[j][i]) are T's rows.
-// PX is persistent like ns_sym_bf16; PX_APPLY issues the next tile's slices
-// after its parameter updates (which load the parameters).
 // ---------------------------------------------------------------------------
-constexpr int PBN = 256;                     // output tile along n
 
 // param[o .. o+valid) += alpha * u (u = 8 bf16 in u8); one rounding to the
 // parameter dtype per element, as torch's foreach add with alpha.  `vec`:
@@ -603,102 +592,66 @@ __device__ __forceinline__ void apply_chunk(typename TP::storage* prm, int64_t o
 }
 
 template <int STAGE, bool TRANS, class TP>
-__global__ __launch_bounds__(NT, 1) void ns_px_bf16(NsArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint16_t lds[LDS_ELEMS];
-  char* stage = reinterpret_cast<char*>(lds + STAGE_OFF);
-  constexpr bool APPLY = STAGE == NS_PX_APPLY;
-
-  const int tiles_j = a.np / PBN;
+__device__ __forceinline__ void px_work(const NsArgs& a, uint16_t* lds, int v) {
+  const int tiles_j = a.np / BN;
   const int tiles = (a.mp / BM) * tiles_j;
-  const int total = 8 * ((a.N + 7) / 8) * tiles;
-  const int64_t pstride = int64_t(a.mp) * PANEL;
-  const uint16_t* Pbase = static_cast<const uint16_t*>(a.a_in);
-  const uint16_t* Xbase = static_cast<const uint16_t*>(a.x_in);
-  const int wn = (threadIdx.x >> 6) & 1;
-
-  // acc = P X + a X (the identity on the P side over the tile's diagonal rows)
-  Pipe<true, IDENT_ROW> p;
-  p.init(pstride, pstride, a.mp / BK, lds, a.ca);
-  auto set = [&](int b, int t) {
-    const int ti = t / tiles_j, tj = t % tiles_j;
-    p.set_tile(Pbase + b * int64_t(a.mp) * a.mp + ti * BM * PANEL,
-               Xbase + b * int64_t(a.mp) * a.np + (tj * PBN / PANEL) * pstride, ti * BM);
-  };
-
   int b, t;
-  int v = next_tile(blockIdx.x, total, tiles, a.N, b, t);
-  if (v >= total) return;
-  set(b, t);
-  p.prologue_first();
-  p.prologue_rest();
-  int extra = 0;
-  f32x16 acc[TM][TM];
-  while (true) {
-    p.run(acc, extra);
-    barrier();  // every wave is done with the ring
-    const int cb = b, cti = t / tiles_j, ctj = t % tiles_j;
-    v = next_tile(v + gridDim.x, total, tiles, a.N, b, t);
-    if (!APPLY && v < total) {
-      set(b, t);
-      p.prologue_first();
+  if (!decode_tile(v, tiles, a.N, b, t)) return;
+  const int ti = t / tiles_j, tc = t % tiles_j;
+  const int r0 = ti * BM, c0 = tc * BN;
+
+  const int64_t pstride = int64_t(a.mp) * PANEL;
+  const uint16_t* P = static_cast<const uint16_t*>(a.a_in) + int64_t(b) * a.mp * a.mp + r0 * PANEL;
+  const uint16_t* X = static_cast<const uint16_t*>(a.x_in) + int64_t(b) * a.mp * a.np + (c0 / PANEL) * pstride;
+  f32x16 acc[TMI][TMJ];
+  // acc = P X + a X (the identity on the P side over the tile's diagonal rows)
+  mainloop<true, IDENT_ROW>(P, X, pstride, a.mp / BK, lds, acc, a.ca, r0);
+
+  const float s = a.scale != nullptr ? a.scale[b] : 1.f;
+  char* stage = reinterpret_cast<char*>(lds);
+  barrier();  // every wave is done with the ring
+  stage_tile(stage, acc, s);
+  barrier();
+  if (STAGE == NS_PX) {
+    // X'[r0 + i][c0 + r] = T[r][i]
+    uint16_t* dst = static_cast<uint16_t*>(a.out) + int64_t(b) * a.mp * a.np + (c0 / PANEL) * pstride +
+                    int64_t(r0) * PANEL;
+    stage_cols(stage, [&](int i, int r, const uint4& u) {
+      *reinterpret_cast<uint4*>(dst + (r >> 5) * pstride + i * PANEL + (r & 31)) = u;
+    });
+    return;
+  }
+  // apply: param += alpha * u; the parameter block is stored (m x n)
+  // untransposed or (n x m) for a tall block
+  auto* prm = reinterpret_cast<typename TP::storage*>(a.blocks[b].param);
+  const float alpha = a.alpha;
+  const int m = a.m, n = a.n;
+  // 16-B vector access: aligned blocks and a row length that keeps chunks aligned
+  const bool vec = a.vec && ((TRANS ? m : n) % 8 == 0);
+  if (TRANS) {
+    const int tid = threadIdx.x;
+    const int c = (tid & 31) * 8;
+    for (int q = 0; q < BN / (NT / 32); ++q) {
+      const int r = q * (NT / 32) + (tid >> 5);  // staged row = X' column = parameter row
+      const int pr = c0 + r, pc = r0 + c;
+      if (pr >= n || pc >= m) continue;
+      const uint4 u8 = *reinterpret_cast<const uint4*>(stage + tile_off(r, c));
+      apply_chunk<TP>(prm, int64_t(pr) * m + pc, u8, alpha, min(8, m - pc), vec);
     }
-    const float s = a.scale != nullptr ? sload_f32(a.scale + cb) : 1.f;
-    const int r0 = cti * BM, c0 = ctj * PBN;
-    const int tid = fresh_tid();
-    const Lane L{tid & 63, (tid >> 6) >> 1, (tid >> 6) & 1};
-    if constexpr (!APPLY) {
-      uint16_t* out = static_cast<uint16_t*>(a.out) + cb * int64_t(a.mp) * a.np;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if (wn == h) stage_half(stage, acc, L, s);
-        barrier();
-        // X'[r0 + i][c0 + 128h + r] = S[r][i]
-        uint16_t* dst = out + ((c0 + 128 * h) / PANEL) * pstride + int64_t(r0) * PANEL;
-        stage_cols(stage, tid, [&](int i, int r, const uint4& u) {
-          *reinterpret_cast<uint4*>(dst + (r >> 5) * pstride + i * PANEL + (r & 31)) = u;
-        });
-        if (h == 0) barrier();
-      }
-      if (v < total) p.prologue_rest();
-      extra = 32;  // stores per thread issued after slice 0
-    } else {
-      // apply: param += alpha * u; the parameter block is stored (m x n)
-      // untransposed or (n x m) for a tall block
-      auto* prm = reinterpret_cast<typename TP::storage*>(a.blocks[cb].param);
-      const float alpha = a.alpha;
-      const int m = a.m, n = a.n;
-      // 16-B vector access: aligned blocks and a row length that keeps chunks aligned
-      const bool vec = a.vec && ((TRANS ? m : n) % 8 == 0);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if (wn == h) stage_half(stage, acc, L, s);
-        barrier();
-        const int cj = c0 + 128 * h;  // first X' column of this half
-        if (TRANS) {
-          const int c = (tid & 31) * 8;
-          for (int q = 0; q < 16; ++q) {
-            const int r = q * 8 + (tid >> 5);  // staged row = X' column = parameter row
-            const int pr = cj + r, pc = r0 + c;
-            if (pr >= n || pc >= m) continue;
-            const uint4 u8 = *reinterpret_cast<const uint4*>(stage + tile_off(r, c));
-            apply_chunk<TP>(prm, int64_t(pr) * m + pc, u8, alpha, min(8, m - pc), vec);
-          }
-        } else {
-          stage_cols(stage, tid, [&](int i, int r, const uint4& u) {
-            const int pr = r0 + i, pc = cj + r;
-            if (pr < m && pc < n) apply_chunk<TP>(prm, int64_t(pr) * n + pc, u, alpha, min(8, n - pc), vec);
-          });
-        }
-        barrier();  // the staging area is reused (next half, or the next tile's slot 3)
-      }
-      if (v < total) {
-        set(b, t);
-        p.prologue_first();
-        p.prologue_rest();
-      }
-      extra = 0;
-    }
-    if (v >= total) break;
+  } else {
+    stage_cols(stage, [&](int i, int r, const uint4& u) {
+      const int pr = r0 + i, pc = c0 + r;
+      if (pr < m && pc < n) apply_chunk<TP>(prm, int64_t(pr) * n + pc, u, alpha, min(8, n - pc), vec);
+    });
+  }
+}
+
+template <int STAGE, bool TRANS, class TP>
+__global__ __launch_bounds__(NT, WG_PER_CU) void ns_px_bf16(NsArgs a, int total) {
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[LDS_ELEMS];
+  for (int v = blockIdx.x; v < total; v += gridDim.x) {
+    px_work<STAGE, TRANS, TP>(a, lds, v);
+    barrier();  // the staging area is read before the next tile's loads refill the ring
   }
 }
 
@@ -788,9 +741,8 @@ __global__ __launch_bounds__(256) void ns_f32(NsArgs a) {
   }
 }
 
-// Persistent grid: one workgroup per CU (each takes all of a CU's LDS), a
-// multiple of 8 so that a workgroup's tiles stay on its XCD.
-int persistent_grid(int total) {
+// Workgroups that fit on the device at once, a multiple of 8.
+int resident_grid(int total) {
   static std::atomic<int> cus_cache[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
@@ -800,8 +752,7 @@ int persistent_grid(int total) {
       cus = 256;
     cus_cache[dev].store(cus, std::memory_order_relaxed);
   }
-  const int g = std::max(8, cus / 8 * 8);
-  return std::min(total, g);
+  return std::min(total, std::max(8, WG_PER_CU * cus / 8 * 8));
 }
 
 template <int STAGE, class TP>
@@ -809,15 +760,17 @@ void launch_bf16(const NsArgs& a, hipStream_t s) {
   const int nb8 = 8 * ((a.N + 7) / 8);
   if constexpr (STAGE == NS_SYRK || STAGE == NS_POLY) {
     const int nt = a.mp / BM;
-    const dim3 grid(persistent_grid(nb8 * (nt * (nt + 1) / 2)));
-    hipLaunchKernelGGL((ns_sym_bf16<STAGE>), grid, dim3(NT), 0, s, a);
+    const int nc = a.mp / BN;
+    const int total = nb8 * (nt * nc - R_SYM * nt * (nt - 1) / 2);
+    hipLaunchKernelGGL((ns_sym_bf16<STAGE>), dim3(resident_grid(total)), dim3(NT), 0, s, a, total);
   } else {
-    const dim3 grid(persistent_grid(nb8 * (a.mp / BM) * (a.np / PBN)));
+    const int total = nb8 * (a.mp / BM) * (a.np / BN);
+    const dim3 grid(resident_grid(total));
     if constexpr (STAGE == NS_PX) {
-      hipLaunchKernelGGL((ns_px_bf16<STAGE, false, TP>), grid, dim3(NT), 0, s, a);
+      hipLaunchKernelGGL((ns_px_bf16<STAGE, false, TP>), grid, dim3(NT), 0, s, a, total);
     } else {
-      if (!a.transposed) hipLaunchKernelGGL((ns_px_bf16<STAGE, false, TP>), grid, dim3(NT), 0, s, a);
-      else hipLaunchKernelGGL((ns_px_bf16<STAGE, true, TP>), grid, dim3(NT), 0, s, a);
+      if (!a.transposed) hipLaunchKernelGGL((ns_px_bf16<STAGE, false, TP>), grid, dim3(NT), 0, s, a, total);
+      else hipLaunchKernelGGL((ns_px_bf16<STAGE, true, TP>), grid, dim3(NT), 0, s, a, total);
     }
   }
 }
@@ -832,7 +785,7 @@ void launch_f32(const NsArgs& a, hipStream_t s) {
 }  // namespace
 
 int ns_tile_m(int ns_dtype) { return ns_dtype == MMUON_BF16 ? BM : FB; }
-int ns_tile_n(int ns_dtype) { return ns_dtype == MMUON_BF16 ? PBN : FB; }
+int ns_tile_n(int ns_dtype) { return ns_dtype == MMUON_BF16 ? 256 : FB; }  // pack tiles 256 columns
 int ns_tile_k(int ns_dtype) { return ns_dtype == MMUON_BF16 ? BK : FK; }
 
 int launch_ns_stage(const NsArgs& a, int stage, int ns_dtype, int param_dtype, hipStream_t s) {
