@@ -80,6 +80,36 @@ __global__ __launch_bounds__(PACK_NT) void pack_rows_kernel(PackArgs a) {
   const int tiles_j = a.np / 256;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float ss = 0.f;
+  if constexpr (PANELS) {
+    const int i = (blockIdx.x / tiles_j) * 32 + wave * 8 + (lane >> 3);
+    const int j0 = (blockIdx.x % tiles_j) * 256 + (lane & 7) * 8;
+    if (a.vec && (blockIdx.x / tiles_j) * 32 + 32 <= a.m && (blockIdx.x % tiles_j) * 256 + 256 <= a.n) {
+      // whole tile inside the block: every load of the thread is issued before
+      // the first store, so the loads overlap instead of waiting one by one
+      float gv[PACK_ITERS][8], bv[PACK_ITERS][8];
+      const int64_t s0 = int64_t(i) * a.n + j0;
+#pragma unroll
+      for (int it = 0; it < PACK_ITERS; ++it) {
+        Vec8<TG>::load(g + s0 + it * 64, gv[it]);
+        Vec8<TB>::load(buf + s0 + it * 64, bv[it]);
+      }
+#pragma unroll
+      for (int it = 0; it < PACK_ITERS; ++it) {
+        float v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          bv[it][q] = momentum_update<TB>(bv[it][q], gv[it][q], a.mu);
+          v[q] = TX::round(bv[it][q]);
+          ss += v[q] * v[q];
+        }
+        Vec8<TB>::store(buf + s0 + it * 64, bv[it]);
+        Vec8<TX>::store(x + TX::xoff(a.mp, a.np, i, j0 + it * 64), v);
+      }
+      const float tot = block_sum<PACK_NT>(ss, red);
+      if (threadIdx.x == 0) a.partial[int64_t(b) * a.nparts + blockIdx.x] = tot;
+      return;
+    }
+  }
 #pragma unroll
   for (int it = 0; it < PACK_ITERS; ++it) {
     int i, j;

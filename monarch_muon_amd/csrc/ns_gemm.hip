@@ -628,6 +628,69 @@ __device__ __forceinline__ void px_work(const NsArgs& a, uint16_t* lds, int v) {
   const int m = a.m, n = a.n;
   // 16-B vector access: aligned blocks and a row length that keeps chunks aligned
   const bool vec = a.vec && ((TRANS ? m : n) % 8 == 0);
+  if constexpr (sizeof(typename TP::storage) == 2) {
+    // bf16 parameters, tile inside the block: load every parameter chunk of this
+    // thread first, so their latencies overlap, then combine and store
+    if (vec && r0 + BM <= m && c0 + BN <= n) {
+      constexpr int CH = BN * BM / 8 / NT;  // 16-B chunks per thread
+      constexpr int BATCH = 8;
+      // threadIdx.x through an opaque move, so these per-lane addresses are formed
+      // here rather than hoisted out of the tile loop (where they would be spilled)
+      int tid;
+      asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"(int(threadIdx.x)));
+      const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+      const int l16 = lane & 15, grp = lane >> 4;
+      // chunk q of this thread: parameter offset, staged row r and column c of
+      // its first element (TRANS: 8 consecutive staged columns; else 8 staged rows)
+      auto chunk = [&](int q, int& r, int& c) -> int64_t {
+        if (TRANS) {
+          r = q * (NT / 32) + (tid >> 5);
+          c = (tid & 31) * 8;
+          return int64_t(c0 + r) * m + r0 + c;
+        }
+        const int task = wave + NWAVES * q;  // the stage_cols mapping
+        c = (task & 15) * 16;                // i0
+        r = (task >> 4) * 32 + grp * 8;
+        return int64_t(r0 + c + l16) * n + c0 + r;
+      };
+#pragma unroll
+      for (int q0 = 0; q0 < CH; q0 += BATCH) {
+        uint4 pv[BATCH];
+#pragma unroll
+        for (int q = 0; q < BATCH; ++q) {
+          int r, c;
+          pv[q] = *reinterpret_cast<const uint4*>(prm + chunk(q0 + q, r, c));
+        }
+#pragma unroll
+        for (int q = 0; q < BATCH; ++q) {
+          int r, c;
+          const int64_t o = chunk(q0 + q, r, c);
+          uint4 u;
+          if (TRANS) {
+            u = *reinterpret_cast<const uint4*>(stage + tile_off(r, c));
+          } else {
+            const int tr = r + (l16 >> 2), tc = c + ((l16 & 3) << 2);
+            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(stage + tile_off(tr, tc)));
+            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(stage + tile_off(tr + 4, tc)));
+            u.x = uint32_t(uint16_t(lo[0])) | (uint32_t(uint16_t(lo[1])) << 16);
+            u.y = uint32_t(uint16_t(lo[2])) | (uint32_t(uint16_t(lo[3])) << 16);
+            u.z = uint32_t(uint16_t(hi[0])) | (uint32_t(uint16_t(hi[1])) << 16);
+            u.w = uint32_t(uint16_t(hi[2])) | (uint32_t(uint16_t(hi[3])) << 16);
+          }
+          const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+          uint32_t pw[4] = {pv[q].x, pv[q].y, pv[q].z, pv[q].w};
+#pragma unroll
+          for (int h = 0; h < 4; ++h) {
+            const float u0 = __uint_as_float(w[h] << 16), u1 = __uint_as_float(w[h] & 0xffff0000u);
+            const float p0 = __uint_as_float(pw[h] << 16), p1 = __uint_as_float(pw[h] & 0xffff0000u);
+            pw[h] = f2bf2(fmaf(alpha, u0, p0), fmaf(alpha, u1, p1));
+          }
+          *reinterpret_cast<uint4*>(prm + o) = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+        }
+      }
+      return;
+    }
+  }
   if (TRANS) {
     const int tid = threadIdx.x;
     const int c = (tid & 31) * 8;
