@@ -303,6 +303,17 @@ struct Pipe {
     }
   }
 
+  // Fragment read G (column fragments first, then row fragments) of k step KK.
+  template <int KK, int G>
+  __device__ __forceinline__ void load_one(int kt, Frags& f) const {
+    const uint16_t* sr = rslot(kt);
+    const uint16_t* sc = sr + RSLICE;
+    if constexpr (G < TMJ)
+      f.c[G] = ROWMAJOR_C ? frag_rowmajor_tr(sc, tfrag[G], KK) : frag_kmajor(sc, kfrag[KK], wn * WN + G * 32);
+    else
+      f.r[G - TMJ] = frag_kmajor(sr, kfrag[KK], wm * WM + (G - TMJ) * 32);
+  }
+
   template <int KK, int F>
   __device__ __forceinline__ void math(const Frags& f, f32x16 (&acc)[TMI][TMJ]) const {
 #pragma unroll
@@ -320,24 +331,34 @@ struct Pipe {
   // MFMAs so the memory pipeline drains while the matrix cores stay busy.
   template <int F>
   __device__ __forceinline__ void body(int kt, Frags& fa, Frags& fb, f32x16 (&acc)[TMI][TMJ]) const {
-    load<1>(kt, fb);
-    math<0, F>(fa, acc);
+    static_assert(TMI * TMJ == 8 && SLICE_DMA <= 8 && TMI + TMJ <= 8, "one read / direct load per MFMA");
+#define MMUON_MFMA(f, g) acc[(g) / TMJ][(g) % TMJ] = mfma(f.r[(g) / TMJ], f.c[(g) % TMJ], acc[(g) / TMJ][(g) % TMJ]);
+    // k step 0 of slice kt; the k step 1 reads of the same slice go out one per MFMA
+#define MMUON_STEP0(g)                                          \
+    MMUON_MFMA(fa, g)                                           \
+    if constexpr ((g) < TMI + TMJ) load_one<1, (g)>(kt, fb);   \
+    __builtin_amdgcn_sched_barrier(0);
+    MMUON_STEP0(0) MMUON_STEP0(1) MMUON_STEP0(2) MMUON_STEP0(3)
+    MMUON_STEP0(4) MMUON_STEP0(5) MMUON_STEP0(6) MMUON_STEP0(7)
+#undef MMUON_STEP0
+    if constexpr (F >= 0) ident<0, F>(fa, acc);
     wait_vm<(NSTAGE - 3) * SLICE_DMA>();  // slice kt+1; the later ones may stay in flight
     barrier();
-    // on the last step this reads a slot whose values are never used
-    load<0>(kt + 1, fa);
+    // k step 1 of slice kt, interleaved with the k step 0 reads of slice kt+1 (on
+    // the last step a slot whose values are never used) and the direct loads of
     // slice kt+NSTAGE-1; near the end a consumed slot is refilled with slice KT-1
     // instead, so every step has the same shape
     const int src = kt + NSTAGE - 1 < KT ? kt + NSTAGE - 1 : KT - 1;
     const int slot = kt + NSTAGE - 1;
-#define MMUON_MFMA_DMA(g)                                                            \
-    acc[(g) / TMJ][(g) % TMJ] = mfma(fb.r[(g) / TMJ], fb.c[(g) % TMJ], acc[(g) / TMJ][(g) % TMJ]); \
-    if constexpr ((g) < SLICE_DMA) issue_one<(g)>(src, slot);                      \
+#define MMUON_STEP1(g)                                          \
+    MMUON_MFMA(fb, g)                                           \
+    if constexpr ((g) < TMI + TMJ) load_one<0, (g)>(kt + 1, fa); \
+    if constexpr ((g) < SLICE_DMA) issue_one<(g)>(src, slot);   \
     __builtin_amdgcn_sched_barrier(0);
-    MMUON_MFMA_DMA(0) MMUON_MFMA_DMA(1) MMUON_MFMA_DMA(2) MMUON_MFMA_DMA(3)
-    MMUON_MFMA_DMA(4) MMUON_MFMA_DMA(5) MMUON_MFMA_DMA(6) MMUON_MFMA_DMA(7)
-#undef MMUON_MFMA_DMA
-    static_assert(TMI * TMJ == 8 && SLICE_DMA <= 8, "one direct load per MFMA of the k step");
+    MMUON_STEP1(0) MMUON_STEP1(1) MMUON_STEP1(2) MMUON_STEP1(3)
+    MMUON_STEP1(4) MMUON_STEP1(5) MMUON_STEP1(6) MMUON_STEP1(7)
+#undef MMUON_STEP1
+#undef MMUON_MFMA
     if constexpr (F >= 0) ident<1, F>(fb, acc);
   }
 
