@@ -11,17 +11,17 @@
 // 1 afterwards.
 //
 // bf16 kernels: v_mfma_f32_32x32x16_bf16, fp32 accumulation, bf16 stage outputs.
-// 256-thread workgroups (4 waves) compute a 256x128 output tile; each wave a
-// 128x64 sub-tile (4x2 MFMA tiles, 128 accumulators).  Two workgroups share a
-// CU (72 KiB of LDS and at most 256 registers per wave each), so one
-// workgroup's epilogue and memory waits overlap the other's MFMAs.  K advances
-// 32 at a time through a 3-slot LDS ring filled by direct global->LDS loads
-// (global_load_lds_dwordx4), one slice in flight ahead of the one in use.
-// SYRK/POLY compute only the tiles on or above the diagonal blocks and write
-// each off-diagonal tile and its mirror.  Every bf16 stack is stored in
-// 32-column panels (panel_off), so a K slice is contiguous in HBM.  The X
-// operand of PX has the contraction along its rows; its slice is staged into LDS
-// as stored and read transposed with ds_read_b64_tr_b16.
+// One 512-thread workgroup (8 waves, 2 per SIMD) per CU computes 256 x 256
+// output tiles, each wave a 128 x 64 sub-tile (4 x 2 MFMA tiles, 128
+// accumulators).  K advances 32 at a time through a 4-slot LDS ring filled by
+// direct global->LDS loads (global_load_lds_dwordx4), two slices in flight
+// behind the one being read; the loads of a step are interleaved with its
+// MFMAs.  The workgroups are persistent and walk the tiles in rounds, all tiles
+// of one block on one XCD.  Every bf16 stack is stored in 32-column panels
+// (panel_off), so a K slice is one contiguous run in HBM.  The symmetric A and
+// P stacks hold only their tiles on and above the diagonal: SYRK and POLY
+// compute and store just those, and their consumers read the missing part as
+// the transpose of the stored part (ds_read_b64_tr_b16), as PX reads X.
 #include <algorithm>
 #include <atomic>
 
@@ -100,6 +100,16 @@ __device__ __forceinline__ void wait_vm() {
   else asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
 }
 
+// threadIdx.x through an opaque move: per-lane addresses formed from it are
+// computed where they are used (once per tile) instead of being hoisted out of
+// the tile loop, where they would hold registers across the main loop or be
+// spilled.
+__device__ __forceinline__ int fresh_tid() {
+  int tid;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"(int(threadIdx.x)));
+  return tid;
+}
+
 typedef __attribute__((address_space(3))) void lds_void;
 
 // LDS byte address of a generic pointer into LDS.
@@ -127,40 +137,18 @@ __device__ __forceinline__ void barrier() {
 }
 
 // ----- LDS layouts --------------------------------------------------------
-// K-major slice [rows][32 k] (consecutive rows of one panel): a row is four
+// K-form slice [rows][32 k] (consecutive rows of one panel): a row is four
 // 16-B chunks; chunk c of row r sits in slot c ^ ((r >> 2) & 3), so the 16 rows
-// read by one quarter-wave's ds_read_b128 cover all 64 banks.
-// X slice of a PX stage [BN/32 panels][32 k][32 columns]: 64-B rows as in HBM; the
-// 4 rows x 64 B a half-wave's ds_read_b64_tr_b16 touches are 256 contiguous
-// bytes, one access per bank.
-
-// Issue one K-major operand slice of 16*4*Q rows at `src` (one contiguous run
-// of the panel).  Wave w, instruction q covers rows 16*(Q*w+q) .. +15 (1 KiB);
-// lane l loads row l/4, chunk (l%4) ^ ((l>>4)&3) (kmajor_lane_offset).
+// read by one quarter-wave's ds_read_b128 cover all 64 banks.  A direct load
+// of 16 rows (1 KiB): lane l loads row l/4, chunk (l%4) ^ ((l>>4)&3)
+// (kmajor_lane_offset).
+// T-form slice [8 panels][32 k][32 columns]: 64-B rows as in HBM, lane l of a
+// direct load takes bytes 16l..16l+15 of the 1 KiB run; the 4 rows x 64 B a
+// half-wave's ds_read_b64_tr_b16 touches are 256 contiguous bytes, one access
+// per bank.
 __device__ __forceinline__ uint32_t kmajor_lane_offset(int lane) {
   const int chunk = (lane & 3) ^ ((lane >> 4) & 3);
   return uint32_t(((lane >> 2) * PANEL + chunk * 8) * 2);
-}
-template <int Q>
-__device__ __forceinline__ void issue_kmajor(const uint16_t* src, uint32_t loff, uint32_t slice, int wave) {
-#pragma unroll
-  for (int q = 0; q < Q; ++q) {
-    const int grp = wave * Q + q;
-    dma16(src + grp * 16 * PANEL, loff, slice + grp * 1024);
-  }
-}
-
-// Issue one X slice of a PX stage: rows k0 .. k0+31 of the BN/32 column panels
-// at src, src + pstride, ... (2 KiB contiguous each).  Wave w, instruction q
-// covers panel g/2, rows 16*(g%2) .. +15 with g = CDMA*w + q; the lane offset
-// is 16*l bytes.
-__device__ __forceinline__ void issue_xslice(const uint16_t* src, int64_t pstride, uint32_t loff,
-                                             uint32_t slice, int wave) {
-#pragma unroll
-  for (int q = 0; q < CDMA; ++q) {
-    const int grp = wave * CDMA + q;
-    dma16(src + (grp >> 1) * pstride + (grp & 1) * 16 * PANEL, loff, slice + grp * 1024);
-  }
 }
 
 // 8-element K-major fragment of a 32-row MFMA operand (rows r0 + lane%32,
@@ -199,8 +187,15 @@ __device__ __forceinline__ bf16x8 frag_rowmajor_tr(const uint16_t* slice, uint32
 }
 
 // ---------------------------------------------------------------------------
-// The pipelined main loop shared by every stage.  ROWMAJOR_C: the column
-// operand is the X stack read transposed (PX stages), else K-major (SYRK/POLY).
+// The pipelined main loop shared by every stage.  Each operand slice (256
+// operand rows x 32 k) is read in one of two forms:
+//   K: K-major, rows of the operand itself (one contiguous 16 KiB run of a panel);
+//   T: transposed, 32 rows of the 8 panels whose columns are the operand's rows
+//      (2 KiB runs), read with ds_read_b64_tr_b16.
+// The X operand of PX is always T.  Gram and polynomial stacks store only the
+// tiles on and above the diagonal, so an operand band R of them is T for the
+// K slices left of its diagonal block (from the stored tile (kb, R)) and K from
+// there on.  A slice pair (row operand, column operand) is KK, KT or TT.
 // ---------------------------------------------------------------------------
 // MFMA operand fragments of one 16-deep k step held by one wave.
 struct Frags {
@@ -226,61 +221,85 @@ __device__ __forceinline__ bf16x8 ident_frag(float v, int kk, int lane) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
-template <bool ROWMAJOR_C, int IDENT = IDENT_NONE>
+enum { OP_K = 0, OP_T = 1, OP_SPLIT = 2 };  // operand form over K: always K, always T, T then K
+enum { M_KK = 0, M_KT = 1, M_TT = 2 };        // forms of one slice pair (row, column)
+constexpr bool row_t(int m) { return m == M_TT; }
+constexpr bool col_t(int m) { return m != M_KK; }
+
+template <int RK, int CK, int IDENT>
 struct Pipe {
-  const uint16_t* rsrc;  // row operand: panel 0, first row of the tile
-  const uint16_t* csrc;  // column operand: panel 0, first row (K-major) / first panel (X)
-  int64_t pstride;       // elements per panel (rows * 32)
+  static_assert(RDMA == 2 && CDMA == 2, "two direct loads per thread and operand slice");
+  static_assert(RK != OP_T && (RK == OP_K || CK != OP_K), "row T only where the column is T");
+  // the last run of slices: column T throughout (PX), else both K
+  static constexpr int ML = CK == OP_T ? M_KT : M_KK;
+  const uint16_t* rsrc_k;  // row operand K form: panel 0 at the operand's first row
+  const uint16_t* rsrc_t;  // row operand T form: row 0 of the first panel holding its rows
+  const uint16_t* csrc_k;
+  const uint16_t* csrc_t;
+  int thr_r, thr_c;        // OP_SPLIT: slices kt < thr are T
+  int64_t pstride;         // elements per panel (rows * 32)
   int KT;
   int wave, lane, wm, wn;
   uint16_t* lds;  // ring slot s at lds + s*SLOT: row-operand slice, then column-operand slice
   uint32_t lds0;  // LDS byte address of lds
-  uint32_t r_loff, c_loff;        // per-lane DMA byte offsets
-  uint32_t kfrag[BK / 16];        // per-lane K-major fragment bases
-  uint32_t tfrag[TMJ];            // per-lane transposed fragment bases (one per column tile)
+  uint32_t k_loff;                // per-lane direct-load byte offset of the K form (T form: 16 * lane)
+  uint32_t kfrag[BK / 16];        // per-lane K-form fragment bases
+  uint32_t tfrag_r, tfrag_c;      // per-lane T-form fragment bases of the wave's first row / column tile
   int diag0;                      // K index of this wave's first identity row / column
   float id_hi, id_lo;             // identity scalar split into two bf16 parts
 
   __device__ __forceinline__ uint16_t* rslot(int kt) const { return lds + (kt % NSTAGE) * SLOT; }
 
-  // Slice src_kt into the ring slot of slice slot_kt.
-  __device__ __forceinline__ void issue(int src_kt, int slot_kt) const {
-    const uint32_t rs = lds0 + (slot_kt % NSTAGE) * SLOT * 2;
-    const uint32_t cs = rs + RSLICE * 2;
-    issue_kmajor<RDMA>(rsrc + src_kt * pstride, r_loff, rs, wave);
-    if (ROWMAJOR_C) issue_xslice(csrc + src_kt * BK * PANEL, pstride, c_loff, cs, wave);
-    else issue_kmajor<CDMA>(csrc + src_kt * pstride, r_loff, cs, wave);
+  __device__ __forceinline__ bool row_is_t(int kt) const { return RK == OP_SPLIT && kt < thr_r; }
+  __device__ __forceinline__ bool col_is_t(int kt) const {
+    return CK == OP_T || (CK == OP_SPLIT && kt < thr_c);
   }
 
-  // Direct load q (0 .. RDMA+CDMA-1) of slice `src_kt` into the ring slot of
-  // slice `slot_kt` (the same slice, except for the harmless refill of a
-  // consumed slot at the end of the loop).
+  // Direct load Q (0, 1: row operand; 2, 3: column operand) of slice src_kt into
+  // the ring slot of slice slot_kt (the same slice, except for the harmless
+  // refill of a consumed slot at the end of the loop).  K form: wave w, load q
+  // covers operand rows 16 (2w + q) .. +15 of the panel (1 KiB); T form: panel
+  // w of the operand, k rows 16q .. 16q+15 of the slice (1 KiB).  Either way the
+  // load lands at byte (2w + q) * 1024 of the operand's slice.
   template <int Q>
   __device__ __forceinline__ void issue_one(int src_kt, int slot_kt) const {
-    const uint32_t rs = lds0 + (slot_kt % NSTAGE) * SLOT * 2;
-    if constexpr (Q < RDMA) {
-      const int grp = wave * RDMA + Q;
-      dma16(rsrc + src_kt * pstride + grp * 16 * PANEL, r_loff, rs + grp * 1024);
-    } else {
-      const int grp = wave * CDMA + (Q - RDMA);
-      const uint32_t cs = rs + RSLICE * 2 + grp * 1024;
-      if (ROWMAJOR_C)
-        dma16(csrc + src_kt * BK * PANEL + (grp >> 1) * pstride + (grp & 1) * 16 * PANEL, c_loff, cs);
-      else
-        dma16(csrc + src_kt * pstride + grp * 16 * PANEL, r_loff, cs);
-    }
+    constexpr int q = Q & 1;
+    const uint32_t dst = lds0 + (slot_kt % NSTAGE) * SLOT * 2 + (Q < 2 ? 0 : RSLICE * 2) + (2 * wave + q) * 1024;
+    const bool t = Q < 2 ? row_is_t(src_kt) : col_is_t(src_kt);
+    const uint16_t* srck = Q < 2 ? rsrc_k : csrc_k;
+    const uint16_t* srct = Q < 2 ? rsrc_t : csrc_t;
+    if (t)
+      dma16(srct + src_kt * (BK * PANEL) + wave * pstride + q * 16 * PANEL, uint32_t(lane) << 4, dst);
+    else
+      dma16(srck + src_kt * pstride + (2 * wave + q) * 16 * PANEL, k_loff, dst);
+  }
+  __device__ __forceinline__ void issue(int src_kt, int slot_kt) const {
+    issue_one<0>(src_kt, slot_kt);
+    issue_one<1>(src_kt, slot_kt);
+    issue_one<2>(src_kt, slot_kt);
+    issue_one<3>(src_kt, slot_kt);
   }
 
-  // Fragment reads of k step KK (0 or 1) of slice kt.
-  template <int KK>
-  __device__ __forceinline__ void load(int kt, Frags& f) const {
+  // Fragment read G (column fragments first, then row fragments) of k step KK
+  // of slice kt in slice-pair form M.
+  template <int KK, int G, int M>
+  __device__ __forceinline__ void load_one(int kt, Frags& f) const {
     const uint16_t* sr = rslot(kt);
     const uint16_t* sc = sr + RSLICE;
-#pragma unroll
-    for (int j = 0; j < TMJ; ++j)
-      f.c[j] = ROWMAJOR_C ? frag_rowmajor_tr(sc, tfrag[j], KK) : frag_kmajor(sc, kfrag[KK], wn * WN + j * 32);
-#pragma unroll
-    for (int i = 0; i < TMI; ++i) f.r[i] = frag_kmajor(sr, kfrag[KK], wm * WM + i * 32);
+    if constexpr (G < TMJ)
+      f.c[G] = col_t(M) ? frag_rowmajor_tr(sc, tfrag_c + G * 2048, KK) : frag_kmajor(sc, kfrag[KK], wn * WN + G * 32);
+    else
+      f.r[G - TMJ] = row_t(M) ? frag_rowmajor_tr(sr, tfrag_r + (G - TMJ) * 2048, KK)
+                              : frag_kmajor(sr, kfrag[KK], wm * WM + (G - TMJ) * 32);
+  }
+  template <int KK, int M>
+  __device__ __forceinline__ void load(int kt, Frags& f) const {
+    load_one<KK, 0, M>(kt, f);
+    load_one<KK, 1, M>(kt, f);
+    load_one<KK, 2, M>(kt, f);
+    load_one<KK, 3, M>(kt, f);
+    load_one<KK, 4, M>(kt, f);
+    load_one<KK, 5, M>(kt, f);
   }
 
   // Identity MFMAs of k step KK when this slice crosses the identity at
@@ -303,40 +322,20 @@ struct Pipe {
     }
   }
 
-  // Fragment read G (column fragments first, then row fragments) of k step KK.
-  template <int KK, int G>
-  __device__ __forceinline__ void load_one(int kt, Frags& f) const {
-    const uint16_t* sr = rslot(kt);
-    const uint16_t* sc = sr + RSLICE;
-    if constexpr (G < TMJ)
-      f.c[G] = ROWMAJOR_C ? frag_rowmajor_tr(sc, tfrag[G], KK) : frag_kmajor(sc, kfrag[KK], wn * WN + G * 32);
-    else
-      f.r[G - TMJ] = frag_kmajor(sr, kfrag[KK], wm * WM + (G - TMJ) * 32);
-  }
-
-  template <int KK, int F>
-  __device__ __forceinline__ void math(const Frags& f, f32x16 (&acc)[TMI][TMJ]) const {
-#pragma unroll
-    for (int i = 0; i < TMI; ++i)
-#pragma unroll
-      for (int j = 0; j < TMJ; ++j) acc[i][j] = mfma(f.r[i], f.c[j], acc[i][j]);
-    if constexpr (F >= 0) ident<KK, F>(f, acc);
-  }
-
-  // Fragments ping-pong at half-slice granularity: the k step 1 reads of slice kt
-  // stream in under the k step 0 MFMAs, and (after the slice-kt+1 barrier) the
-  // k step 0 reads of slice kt+1 under the k step 1 MFMAs.  At the barrier of
-  // step kt every wave has consumed slice kt-1, so its slot takes slice
-  // kt+NSTAGE-1; those direct loads are interleaved one by one with the k step 1
-  // MFMAs so the memory pipeline drains while the matrix cores stay busy.
-  template <int F>
+  // Step kt: slice kt is consumed in form M, slice kt+1 (its k step 0 fragments)
+  // is read in form MN.  Fragments ping-pong at half-slice granularity: the k
+  // step 1 reads of slice kt go out one per MFMA of its k step 0, and (after
+  // the slice-kt+1 barrier) the k step 0 reads of slice kt+1 one per MFMA of
+  // the k step 1.  At the barrier of step kt every wave has consumed slice
+  // kt-1, so its slot takes slice kt+NSTAGE-1; those direct loads are
+  // interleaved one by one with the k step 1 MFMAs as well.
+  template <int M, int MN, int F>
   __device__ __forceinline__ void body(int kt, Frags& fa, Frags& fb, f32x16 (&acc)[TMI][TMJ]) const {
     static_assert(TMI * TMJ == 8 && SLICE_DMA <= 8 && TMI + TMJ <= 8, "one read / direct load per MFMA");
 #define MMUON_MFMA(f, g) acc[(g) / TMJ][(g) % TMJ] = mfma(f.r[(g) / TMJ], f.c[(g) % TMJ], acc[(g) / TMJ][(g) % TMJ]);
-    // k step 0 of slice kt; the k step 1 reads of the same slice go out one per MFMA
-#define MMUON_STEP0(g)                                          \
-    MMUON_MFMA(fa, g)                                           \
-    if constexpr ((g) < TMI + TMJ) load_one<1, (g)>(kt, fb);   \
+#define MMUON_STEP0(g)                                            \
+    MMUON_MFMA(fa, g)                                             \
+    if constexpr ((g) < TMI + TMJ) load_one<1, (g), M>(kt, fb);   \
     __builtin_amdgcn_sched_barrier(0);
     MMUON_STEP0(0) MMUON_STEP0(1) MMUON_STEP0(2) MMUON_STEP0(3)
     MMUON_STEP0(4) MMUON_STEP0(5) MMUON_STEP0(6) MMUON_STEP0(7)
@@ -344,16 +343,15 @@ struct Pipe {
     if constexpr (F >= 0) ident<0, F>(fa, acc);
     wait_vm<(NSTAGE - 3) * SLICE_DMA>();  // slice kt+1; the later ones may stay in flight
     barrier();
-    // k step 1 of slice kt, interleaved with the k step 0 reads of slice kt+1 (on
-    // the last step a slot whose values are never used) and the direct loads of
-    // slice kt+NSTAGE-1; near the end a consumed slot is refilled with slice KT-1
-    // instead, so every step has the same shape
+    // on the last step slice kt+1 does not exist and the reads of its slot go
+    // unused; near the end a consumed slot is refilled with slice KT-1 so every
+    // step has the same shape
     const int src = kt + NSTAGE - 1 < KT ? kt + NSTAGE - 1 : KT - 1;
     const int slot = kt + NSTAGE - 1;
-#define MMUON_STEP1(g)                                          \
-    MMUON_MFMA(fb, g)                                           \
-    if constexpr ((g) < TMI + TMJ) load_one<0, (g)>(kt + 1, fa); \
-    if constexpr ((g) < SLICE_DMA) issue_one<(g)>(src, slot);   \
+#define MMUON_STEP1(g)                                              \
+    MMUON_MFMA(fb, g)                                               \
+    if constexpr ((g) < TMI + TMJ) load_one<0, (g), MN>(kt + 1, fa); \
+    if constexpr ((g) < SLICE_DMA) issue_one<(g)>(src, slot);       \
     __builtin_amdgcn_sched_barrier(0);
     MMUON_STEP1(0) MMUON_STEP1(1) MMUON_STEP1(2) MMUON_STEP1(3)
     MMUON_STEP1(4) MMUON_STEP1(5) MMUON_STEP1(6) MMUON_STEP1(7)
@@ -362,48 +360,78 @@ struct Pipe {
     if constexpr (F >= 0) ident<1, F>(fb, acc);
   }
 
+  // Slices a .. b-1 in form M (b > a), the last of them reading slice b in form MN.
+  template <int M, int MN>
+  __device__ __forceinline__ void run_span(int a, int b, Frags& fa, Frags& fb, f32x16 (&acc)[TMI][TMJ]) const {
+    for (int kt = a; kt < b - 1; ++kt) body<M, M, -1>(kt, fa, fb, acc);
+    body<M, MN, -1>(b - 1, fa, fb, acc);
+  }
+
   __device__ __forceinline__ void run(f32x16 (&acc)[TMI][TMJ]) const {
 #pragma unroll
     for (int i = 0; i < TMI; ++i)
 #pragma unroll
       for (int j = 0; j < TMJ; ++j) acc[i][j] = f32x16{};
+    // slice runs: TT [0, t1), KT [t1, t2), then ML to the end
+    const int t1 = RK == OP_SPLIT ? thr_r : 0;
+    const int t2 = CK == OP_SPLIT ? thr_c : (CK == OP_T ? t1 : 0);
     // slices 0 .. NSTAGE-2 (beyond the last slice: refills with slice KT-1)
 #pragma unroll
     for (int q = 0; q < NSTAGE - 1; ++q) issue(q < KT ? q : KT - 1, q);
     wait_vm<(NSTAGE - 2) * SLICE_DMA>();  // slice 0 visible, the others may stay in flight
     barrier();
     Frags fa, fb;
-    load<0>(0, fa);
+    if (t1 > 0) load<0, M_TT>(0, fa);
+    else if (CK == OP_SPLIT && t2 > 0) load<0, M_KT>(0, fa);
+    else load<0, ML>(0, fa);
+    if constexpr (RK == OP_SPLIT) {
+      if (t1 > 0) {
+        if (CK == OP_SPLIT && t2 == t1) run_span<M_TT, M_KK>(0, t1, fa, fb, acc);
+        else run_span<M_TT, M_KT>(0, t1, fa, fb, acc);
+      }
+    }
+    if constexpr (CK == OP_SPLIT) {
+      if (t2 > t1) run_span<M_KT, M_KK>(t1, t2, fa, fb, acc);
+    }
+    // the last run (every remaining slice in form ML), with the identity steps
+    const int k0 = t2;
     if constexpr (IDENT == IDENT_NONE) {
-      for (int kt = 0; kt < KT; ++kt) body<-1>(kt, fa, fb, acc);
+      for (int kt = k0; kt < KT; ++kt) body<ML, ML, -1>(kt, fa, fb, acc);
     } else {
       // the slices starting at diag0 cross this wave's identity fragments in
-      // order (diag0 is a multiple of the wave's extent along K)
+      // order (diag0 is a multiple of the wave's extent along K and lies in
+      // the last run)
       constexpr int NI = IDENT == IDENT_ROW ? TMI : TMJ;
       const int kd = diag0 / BK;
-      for (int kt = 0; kt < kd; ++kt) body<-1>(kt, fa, fb, acc);
-      body<0>(kd, fa, fb, acc);
-      body<1>(kd + 1, fa, fb, acc);
+      for (int kt = k0; kt < kd; ++kt) body<ML, ML, -1>(kt, fa, fb, acc);
+      body<ML, ML, 0>(kd, fa, fb, acc);
+      body<ML, ML, 1>(kd + 1, fa, fb, acc);
       if constexpr (NI == 4) {
-        body<2>(kd + 2, fa, fb, acc);
-        body<3>(kd + 3, fa, fb, acc);
+        body<ML, ML, 2>(kd + 2, fa, fb, acc);
+        body<ML, ML, 3>(kd + 3, fa, fb, acc);
       }
-      for (int kt = kd + NI; kt < KT; ++kt) body<-1>(kt, fa, fb, acc);
+      for (int kt = kd + NI; kt < KT; ++kt) body<ML, ML, -1>(kt, fa, fb, acc);
     }
     wait_vm<0>();  // the refills of the last two steps land before the ring is reused
   }
 };
 
-// rsrc / csrc: panel-layout operands at the tile's first row (first panel for
-// the X operand of PX); pstride: elements per panel.  ident_v: the identity
+// Operand sources: *_k the K form (panel 0 at the operand's first row), *_t the
+// T form (row 0 of the first panel holding the operand's rows); thr_*: slices
+// kt < thr are T (OP_SPLIT); pstride: elements per panel.  ident_v: the identity
 // scalar; diag: K index of the tile's first row (IDENT_ROW) or column (IDENT_COL).
-template <bool ROWMAJOR_C, int IDENT = IDENT_NONE>
-__device__ __forceinline__ void mainloop(const uint16_t* rsrc, const uint16_t* csrc, int64_t pstride,
-                                         int KT, uint16_t* lds, f32x16 (&acc)[TMI][TMJ],
+template <int RK, int CK, int IDENT = IDENT_NONE>
+__device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t* rsrc_t, int thr_r,
+                                         const uint16_t* csrc_k, const uint16_t* csrc_t, int thr_c,
+                                         int64_t pstride, int KT, uint16_t* lds, f32x16 (&acc)[TMI][TMJ],
                                          float ident_v = 0.f, int diag = 0) {
-  Pipe<ROWMAJOR_C, IDENT> p;
-  p.rsrc = rsrc;
-  p.csrc = csrc;
+  Pipe<RK, CK, IDENT> p;
+  p.rsrc_k = rsrc_k;
+  p.rsrc_t = rsrc_t;
+  p.csrc_k = csrc_k;
+  p.csrc_t = csrc_t;
+  p.thr_r = thr_r;
+  p.thr_c = thr_c;
   p.pstride = pstride;
   p.KT = KT;
   p.lane = threadIdx.x & 63;
@@ -412,12 +440,11 @@ __device__ __forceinline__ void mainloop(const uint16_t* rsrc, const uint16_t* c
   p.wn = p.wave % NWN;
   p.lds = lds;
   p.lds0 = lds_addr(lds);
-  p.r_loff = kmajor_lane_offset(p.lane);
-  p.c_loff = ROWMAJOR_C ? uint32_t(p.lane * 16) : p.r_loff;
+  p.k_loff = kmajor_lane_offset(p.lane);
 #pragma unroll
   for (int kk = 0; kk < BK / 16; ++kk) p.kfrag[kk] = kmajor_frag_base(kk, p.lane);
-#pragma unroll
-  for (int j = 0; j < TMJ; ++j) p.tfrag[j] = rowmajor_frag_base(p.wn * TMJ + j, p.lane);
+  p.tfrag_r = rowmajor_frag_base(p.wm * TMI, p.lane);
+  p.tfrag_c = rowmajor_frag_base(p.wn * TMJ, p.lane);
   p.diag0 = diag + (IDENT == IDENT_ROW ? p.wm * WM : p.wn * WN);
   p.id_hi = rbf(ident_v);
   p.id_lo = ident_v - p.id_hi;
@@ -442,7 +469,8 @@ __device__ __forceinline__ uint32_t tile_off(int r, int c) {
 // scaled by f before the bf16 rounding.  Lane geometry: the lane holds column
 // j = 64 wn + 32 tj + lane%32 and rows i = 128 wm + 32 ti + 8 qg + 4 (lane/32) + e.
 __device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI][TMJ], float f) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = fresh_tid();
+  const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / NWN, wn = wave % NWN;
 #pragma unroll
   for (int i = 0; i < TMI; ++i) {
@@ -466,7 +494,8 @@ __device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI]
 // first column panel (panel stride pstride).  One wave instruction writes rows
 // 16u .. 16u+15 of one panel (1 KiB contiguous).
 __device__ __forceinline__ void stage_rows(const char* stage, uint16_t* dst, int64_t pstride) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = fresh_tid();
+  const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll 4
   for (int it = 0; it < 8 * (BN / 16) / NWAVES; ++it) {
     const int u = wave + NWAVES * it;  // 8 panels x BN/16 row blocks
@@ -486,7 +515,8 @@ __device__ __forceinline__ void stage_rows(const char* stage, uint16_t* dst, int
 // 1 KiB.  `fn(i, r, uint4)` consumes destination row i, columns r..r+7.
 template <class Fn>
 __device__ __forceinline__ void stage_cols(const char* stage, Fn&& fn) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = fresh_tid();
+  const int lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, grp = lane >> 4;
 #pragma unroll 2
   for (int task = wave; task < 16 * (BN / 32); task += NWAVES) {
@@ -504,11 +534,13 @@ __device__ __forceinline__ void stage_cols(const char* stage, Fn&& fn) {
 }
 
 // ---------------------------------------------------------------------------
-// SYRK / POLY: symmetric m x m outputs, both operands K-major rows.  A tile is
-// a 256-row band ti x 128-column band tc with tc >= 2 ti; the two tiles that
-// cover a diagonal 256 x 256 block write it directly, every other tile writes
-// itself and its mirror.
+// SYRK / POLY: symmetric m x m outputs of which only the 256 x 256 tiles on and
+// above the diagonal are computed and stored (tile ti x tc, tc >= ti; a
+// diagonal tile in full).  SYRK reads X (K form); POLY reads the stored upper
+// tiles of A (operand band R: T form left of its diagonal block, K form from
+// there on).
 // ---------------------------------------------------------------------------
+static_assert(BM == BN, "square tiles: a symmetric tile is either diagonal or strictly upper");
 template <int STAGE>
 __device__ __forceinline__ void sym_work(const NsArgs& a, uint16_t* lds, int v) {
   const int nt = a.mp / BM, nc = a.mp / BN;
@@ -531,9 +563,11 @@ __device__ __forceinline__ void sym_work(const NsArgs& a, uint16_t* lds, int v) 
   const int r0 = ti * BM, c0 = tc * BN;
   f32x16 acc[TMI][TMJ];
   if (STAGE == NS_SYRK)
-    mainloop<false>(src + r0 * PANEL, src + c0 * PANEL, pstride, K / BK, lds, acc);
+    mainloop<OP_K, OP_K>(src + r0 * PANEL, nullptr, 0, src + c0 * PANEL, nullptr, 0, pstride, K / BK, lds, acc);
   else  // acc = A A + (b/c) A, so P = c acc = b A + c A A
-    mainloop<false, IDENT_COL>(src + r0 * PANEL, src + c0 * PANEL, pstride, K / BK, lds, acc, a.cb / a.cc, c0);
+    mainloop<OP_SPLIT, OP_SPLIT, IDENT_COL>(src + r0 * PANEL, src + (r0 / PANEL) * pstride, r0 / BK,
+                                            src + c0 * PANEL, src + (c0 / PANEL) * pstride, c0 / BK,
+                                            pstride, K / BK, lds, acc, a.cb / a.cc, c0);
 
   float f = STAGE == NS_POLY ? a.cc : 1.f;  // SYRK: s^2 on the first iteration
   if (STAGE == NS_SYRK && a.scale != nullptr) {
@@ -545,17 +579,16 @@ __device__ __forceinline__ void sym_work(const NsArgs& a, uint16_t* lds, int v) 
   barrier();  // every wave is done with the ring
   stage_tile(stage, acc, f);
   barrier();
-  const bool diag = tc < R_SYM * (ti + 1);  // the tile meets a diagonal BM x BM block
-  // direct tile C[r0 + i][c0 + r] = T[r][i] (a square diagonal tile is written
-  // once, through its mirror)
-  if (R_SYM > 1 || !diag) {
+  if (tc != ti) {
+    // upper tile C[r0 + i][c0 + r] = T[r][i]
     uint16_t* dst = out + (c0 / PANEL) * pstride + int64_t(r0) * PANEL;
     stage_cols(stage, [&](int i, int r, const uint4& u) {
       *reinterpret_cast<uint4*>(dst + (r >> 5) * pstride + i * PANEL + (r & 31)) = u;
     });
+  } else {
+    // diagonal tile in full, through its mirror C[r0 + r][r0 + i] = T[r][i]
+    stage_rows(stage, out + (r0 / PANEL) * pstride + int64_t(r0) * PANEL, pstride);
   }
-  // mirror C[c0 + r][r0 + i] = T[r][i]
-  if (R_SYM == 1 || !diag) stage_rows(stage, out + (r0 / PANEL) * pstride + int64_t(c0) * PANEL, pstride);
 }
 
 template <int STAGE>
@@ -568,7 +601,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void ns_sym_bf16(NsArgs a, int total
 }
 
 // ---------------------------------------------------------------------------
-// PX / PX_APPLY: X' = s (a X + P X), m x n output tile (256 x 128), K = m.
+// PX / PX_APPLY: X' = s (a X + P X), m x n output tile (256 x 256), K = m.
 // D[i][j] in registers (lane holds column j, rows i..i+3); the a X term enters
 // the accumulation as (a I) X.  T[j][i] = X'[r0 + i][c0 + j] is staged in LDS;
 // X' rows (PX, and the parameter rows of an untransposed block) are T's
@@ -622,11 +655,12 @@ __device__ __forceinline__ void px_work(const NsArgs& a, uint16_t* lds, int v) {
   const int r0 = ti * BM, c0 = tc * BN;
 
   const int64_t pstride = int64_t(a.mp) * PANEL;
-  const uint16_t* P = static_cast<const uint16_t*>(a.a_in) + int64_t(b) * a.mp * a.mp + r0 * PANEL;
+  const uint16_t* P = static_cast<const uint16_t*>(a.a_in) + int64_t(b) * a.mp * a.mp;
   const uint16_t* X = static_cast<const uint16_t*>(a.x_in) + int64_t(b) * a.mp * a.np + (c0 / PANEL) * pstride;
   f32x16 acc[TMI][TMJ];
   // acc = P X + a X (the identity on the P side over the tile's diagonal rows)
-  mainloop<true, IDENT_ROW>(P, X, pstride, a.mp / BK, lds, acc, a.ca, r0);
+  mainloop<OP_SPLIT, OP_T, IDENT_ROW>(P + r0 * PANEL, P + (r0 / PANEL) * pstride, r0 / BK, nullptr, X, 0,
+                                      pstride, a.mp / BK, lds, acc, a.ca, r0);
 
   const float s = a.scale != nullptr ? a.scale[b] : 1.f;
   char* stage = reinterpret_cast<char*>(lds);
@@ -655,10 +689,7 @@ __device__ __forceinline__ void px_work(const NsArgs& a, uint16_t* lds, int v) {
     if (vec && r0 + BM <= m && c0 + BN <= n) {
       constexpr int CH = BN * BM / 8 / NT;  // 16-B chunks per thread
       constexpr int BATCH = 8;
-      // threadIdx.x through an opaque move, so these per-lane addresses are formed
-      // here rather than hoisted out of the tile loop (where they would be spilled)
-      int tid;
-      asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"(int(threadIdx.x)));
+      const int tid = fresh_tid();
       const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
       const int l16 = lane & 15, grp = lane >> 4;
       // chunk q of this thread: parameter offset, staged row r and column c of
