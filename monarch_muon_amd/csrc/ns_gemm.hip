@@ -203,23 +203,12 @@ struct Frags {
   bf16x8 c[TMJ];
 };
 
-// Identity fragments: IDENT_ROW adds v*I on the row-operand side (acc += v X
-// over the K slices that cross the tile's diagonal rows), IDENT_COL on the
-// column-operand side (acc += v A).  v is split into two bf16 parts (hi + lo)
-// so the identity term keeps ~16 bits; the products are exact and accumulate
-// in fp32 with the rest of the dot product.
+// Identity terms folded into the accumulation: IDENT_ROW adds v X (X: the
+// column operand) over the K slices that cross the tile's diagonal rows,
+// IDENT_COL adds v A (A: the row operand) over those that cross its diagonal
+// columns.  The values are taken from the slice in LDS and enter the fp32
+// accumulators by FMA (Pipe::ident_add).
 enum { IDENT_NONE = 0, IDENT_ROW = 1, IDENT_COL = 2 };
-
-__device__ __forceinline__ bf16x8 ident_frag(float v, int kk, int lane) {
-  // lane holds row (or column) lane%32 and k = 16*kk + 8*(lane/32) + t
-  typedef short i16x8 __attribute__((ext_vector_type(8)));
-  const uint16_t h = f2bf(v);
-  i16x8 r = {0, 0, 0, 0, 0, 0, 0, 0};
-  const int t = (lane & 31) - 16 * kk - 8 * (lane >> 5);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = (t == e) ? short(h) : short(0);
-  return __builtin_bit_cast(bf16x8, r);
-}
 
 enum { OP_K = 0, OP_T = 1, OP_SPLIT = 2 };  // operand form over K: always K, always T, T then K
 enum { M_KK = 0, M_KT = 1, M_TT = 2 };        // forms of one slice pair (row, column)
@@ -246,7 +235,7 @@ struct Pipe {
   uint32_t kfrag[BK / 16];        // per-lane K-form fragment bases
   uint32_t tfrag_r, tfrag_c;      // per-lane T-form fragment bases of the wave's first row / column tile
   int diag0;                      // K index of this wave's first identity row / column
-  float id_hi, id_lo;             // identity scalar split into two bf16 parts
+  float id_v;                     // identity scalar
 
   __device__ __forceinline__ uint16_t* rslot(int kt) const { return lds + (kt % NSTAGE) * SLOT; }
 
@@ -302,23 +291,44 @@ struct Pipe {
     load_one<KK, 5, M>(kt, f);
   }
 
-  // Identity MFMAs of k step KK when this slice crosses the identity at
-  // fragment F (32 rows/columns); the identity fragments are built on the spot.
-  template <int KK, int F>
-  __device__ __forceinline__ void ident(const Frags& f, f32x16 (&acc)[TMI][TMJ]) const {
-    const bf16x8 ih = ident_frag(id_hi, KK, lane), il = ident_frag(id_lo, KK, lane);
+  // Identity term of slice kt, which crosses this wave's identity at tile F.
+  // The accumulator of a 32 x 32 tile holds, in lane l, column l%32 and rows
+  // 8q + 4(l/32) + e (value 4q + e); ds_read_b64_tr_b16 gives lane l of a
+  // 16-lane group the four values of one column in four consecutive rows, so
+  // one read per q delivers the lane's four rows.
+  //   IDENT_ROW: acc[F][j] += v X[k][c], k = the accumulator row (the slice's
+  //     row k%32), c its column; X slice in T form, byte p*2048 + k*64 + c*2.
+  //   IDENT_COL: acc[i][F] += v A[r][k], k = the accumulator column; A slice
+  //     in K form, byte r*64 + ((k/8) ^ ((r/4)%4))*16 + (k%8)*2, the same
+  //     chunk order for the four rows r of a read.
+  template <int F>
+  __device__ __forceinline__ void ident_add(int kt, f32x16 (&acc)[TMI][TMJ]) const {
+    const int l16 = lane & 15, g = lane >> 4;
+    const int k16 = 16 * (g & 1) + 4 * (l16 & 3);  // first column of the lane's 8-byte chunk
     if constexpr (IDENT == IDENT_ROW) {
+      const char* sc = reinterpret_cast<const char*>(rslot(kt) + RSLICE);
+      const uint32_t base = uint32_t((4 * (g >> 1) + (l16 >> 2)) * 64 + k16 * 2);
 #pragma unroll
-      for (int j = 0; j < TMJ; ++j) {
-        acc[F][j] = mfma(ih, f.c[j], acc[F][j]);
-        acc[F][j] = mfma(il, f.c[j], acc[F][j]);
-      }
+      for (int j = 0; j < TMJ; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_i16x4*)(sc + (wn * TMJ + j) * 2048 + q * 8 * 64 + base));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[F][j][4 * q + e] = fmaf(id_v, bf2f(uint16_t(v[e])), acc[F][j][4 * q + e]);
+        }
     } else {
+      const char* sr = reinterpret_cast<const char*>(rslot(kt));
 #pragma unroll
-      for (int i = 0; i < TMI; ++i) {
-        acc[i][F] = mfma(f.r[i], ih, acc[i][F]);
-        acc[i][F] = mfma(f.r[i], il, acc[i][F]);
-      }
+      for (int i = 0; i < TMI; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int rb = wm * WM + 32 * i + 8 * q + 4 * (g >> 1);  // first of the four rows
+          const uint32_t off = uint32_t((rb + (l16 >> 2)) * 64 + (((k16 >> 3) ^ ((rb >> 2) & 3)) << 4) + (k16 & 7) * 2);
+          const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sr + off));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[i][F][4 * q + e] = fmaf(id_v, bf2f(uint16_t(v[e])), acc[i][F][4 * q + e]);
+        }
     }
   }
 
@@ -328,7 +338,8 @@ struct Pipe {
   // the slice-kt+1 barrier) the k step 0 reads of slice kt+1 one per MFMA of
   // the k step 1.  At the barrier of step kt every wave has consumed slice
   // kt-1, so its slot takes slice kt+NSTAGE-1; those direct loads are
-  // interleaved one by one with the k step 1 MFMAs as well.
+  // interleaved one by one with the k step 1 MFMAs as well.  F >= 0: the
+  // slice crosses this wave's identity at tile F (ident_add).
   template <int M, int MN, int F>
   __device__ __forceinline__ void body(int kt, Frags& fa, Frags& fb, f32x16 (&acc)[TMI][TMJ]) const {
     static_assert(TMI * TMJ == 8 && SLICE_DMA <= 8 && TMI + TMJ <= 8, "one read / direct load per MFMA");
@@ -340,7 +351,6 @@ struct Pipe {
     MMUON_STEP0(0) MMUON_STEP0(1) MMUON_STEP0(2) MMUON_STEP0(3)
     MMUON_STEP0(4) MMUON_STEP0(5) MMUON_STEP0(6) MMUON_STEP0(7)
 #undef MMUON_STEP0
-    if constexpr (F >= 0) ident<0, F>(fa, acc);
     wait_vm<(NSTAGE - 3) * SLICE_DMA>();  // slice kt+1; the later ones may stay in flight
     barrier();
     // on the last step slice kt+1 does not exist and the reads of its slot go
@@ -357,7 +367,8 @@ struct Pipe {
     MMUON_STEP1(4) MMUON_STEP1(5) MMUON_STEP1(6) MMUON_STEP1(7)
 #undef MMUON_STEP1
 #undef MMUON_MFMA
-    if constexpr (F >= 0) ident<1, F>(fb, acc);
+    // the slot of slice kt is refilled only after the next barrier
+    if constexpr (F >= 0) ident_add<F>(kt, acc);
   }
 
   // Slices a .. b-1 in form M (b > a), the last of them reading slice b in form MN.
@@ -398,7 +409,7 @@ struct Pipe {
     if constexpr (IDENT == IDENT_NONE) {
       for (int kt = k0; kt < KT; ++kt) body<ML, ML, -1>(kt, fa, fb, acc);
     } else {
-      // the slices starting at diag0 cross this wave's identity fragments in
+      // the slices starting at diag0 cross this wave's identity tiles in
       // order (diag0 is a multiple of the wave's extent along K and lies in
       // the last run)
       constexpr int NI = IDENT == IDENT_ROW ? TMI : TMJ;
@@ -446,8 +457,7 @@ __device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t*
   p.tfrag_r = rowmajor_frag_base(p.wm * TMI, p.lane);
   p.tfrag_c = rowmajor_frag_base(p.wn * TMJ, p.lane);
   p.diag0 = diag + (IDENT == IDENT_ROW ? p.wm * WM : p.wn * WN);
-  p.id_hi = rbf(ident_v);
-  p.id_lo = ident_v - p.id_hi;
+  p.id_v = ident_v;
   p.run(acc);
 }
 
@@ -658,7 +668,7 @@ __device__ __forceinline__ void px_work(const NsArgs& a, uint16_t* lds, int v) {
   const uint16_t* P = static_cast<const uint16_t*>(a.a_in) + int64_t(b) * a.mp * a.mp;
   const uint16_t* X = static_cast<const uint16_t*>(a.x_in) + int64_t(b) * a.mp * a.np + (c0 / PANEL) * pstride;
   f32x16 acc[TMI][TMJ];
-  // acc = P X + a X (the identity on the P side over the tile's diagonal rows)
+  // acc = P X + a X (the a X term added from the X slices of the tile's diagonal rows)
   mainloop<OP_SPLIT, OP_T, IDENT_ROW>(P + r0 * PANEL, P + (r0 / PANEL) * pstride, r0 / BK, nullptr, X, 0,
                                       pstride, a.mp / BK, lds, acc, a.ca, r0);
 
