@@ -378,6 +378,26 @@ struct Pipe {
     body<M, MN, -1>(b - 1, fa, fb, acc);
   }
 
+  // The direct loads and barriers of run() without the matrix work: a wave
+  // whose sub-tile is not needed keeps the workgroup's ring filled.
+  __device__ __forceinline__ void run_loads_only(f32x16 (&acc)[TMI][TMJ]) const {
+#pragma unroll
+    for (int i = 0; i < TMI; ++i)
+#pragma unroll
+      for (int j = 0; j < TMJ; ++j) acc[i][j] = f32x16{};
+#pragma unroll
+    for (int q = 0; q < NSTAGE - 1; ++q) issue(q < KT ? q : KT - 1, q);
+    wait_vm<(NSTAGE - 2) * SLICE_DMA>();
+    barrier();
+    for (int kt = 0; kt < KT; ++kt) {
+      wait_vm<(NSTAGE - 3) * SLICE_DMA>();
+      barrier();
+      const int src = kt + NSTAGE - 1 < KT ? kt + NSTAGE - 1 : KT - 1;
+      issue(src, kt + NSTAGE - 1);
+    }
+    wait_vm<0>();
+  }
+
   __device__ __forceinline__ void run(f32x16 (&acc)[TMI][TMJ]) const {
 #pragma unroll
     for (int i = 0; i < TMI; ++i)
@@ -430,12 +450,13 @@ struct Pipe {
 // Operand sources: *_k the K form (panel 0 at the operand's first row), *_t the
 // T form (row 0 of the first panel holding the operand's rows); thr_*: slices
 // kt < thr are T (OP_SPLIT); pstride: elements per panel.  ident_v: the identity
-// scalar; diag: K index of the tile's first row (IDENT_ROW) or column (IDENT_COL).
+// scalar; diag: K index of the tile's first row (IDENT_ROW) or column (IDENT_COL);
+// skip (wave-uniform): this wave only issues its share of the direct loads.
 template <int RK, int CK, int IDENT = IDENT_NONE>
 __device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t* rsrc_t, int thr_r,
                                          const uint16_t* csrc_k, const uint16_t* csrc_t, int thr_c,
                                          int64_t pstride, int KT, uint16_t* lds, f32x16 (&acc)[TMI][TMJ],
-                                         float ident_v = 0.f, int diag = 0) {
+                                         float ident_v = 0.f, int diag = 0, bool skip = false) {
   Pipe<RK, CK, IDENT> p;
   p.rsrc_k = rsrc_k;
   p.rsrc_t = rsrc_t;
@@ -458,7 +479,8 @@ __device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t*
   p.tfrag_c = rowmajor_frag_base(p.wn * TMJ, p.lane);
   p.diag0 = diag + (IDENT == IDENT_ROW ? p.wm * WM : p.wn * WN);
   p.id_v = ident_v;
-  p.run(acc);
+  if (skip) p.run_loads_only(acc);
+  else p.run(acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -475,13 +497,37 @@ __device__ __forceinline__ uint32_t tile_off(int r, int c) {
   return uint32_t(r * 512 + ((((c >> 3) ^ g)) << 4) | ((c & 7) << 1));
 }
 
+// Waves of a diagonal tile of a symmetric product: a sub-tile strictly below
+// the tile's diagonal is the transpose of one strictly above it.
+__device__ __forceinline__ bool below_diag(int wm, int wn) { return (wn + 1) * WN <= wm * WM; }
+__device__ __forceinline__ bool above_diag(int wm, int wn) { return wn * WN >= (wm + 1) * WM; }
+static_assert(WM == 2 * WN && BM == 2 * WM, "the sub-tiles below the diagonal mirror those above it");
+
 // D[i][j] accumulators of this wave -> T[j][i] in the staging area, each value
 // scaled by f before the bf16 rounding.  Lane geometry: the lane holds column
 // j = 64 wn + 32 tj + lane%32 and rows i = 128 wm + 32 ti + 8 qg + 4 (lane/32) + e.
-__device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI][TMJ], float f) {
+// diag: a diagonal tile of a symmetric product whose waves below the diagonal
+// computed nothing; the waves above it also write T[i][j] = D[i][j] there.
+__device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI][TMJ], float f,
+                                           bool diag = false) {
   const int tid = fresh_tid();
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / NWN, wn = wave % NWN;
+  if (diag && below_diag(wm, wn)) return;
+  if (diag && above_diag(wm, wn)) {
+#pragma unroll
+    for (int i = 0; i < TMI; ++i)
+#pragma unroll
+      for (int j = 0; j < TMJ; ++j)
+#pragma unroll
+        for (int qg = 0; qg < 4; ++qg)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int row = wm * WM + i * 32 + qg * 8 + (lane >> 5) * 4 + e;
+            const int col = wn * WN + j * 32 + (lane & 31);
+            *reinterpret_cast<uint16_t*>(stage + tile_off(row, col)) = f2bf(f * acc[i][j][qg * 4 + e]);
+          }
+  }
 #pragma unroll
   for (int i = 0; i < TMI; ++i) {
 #pragma unroll
@@ -571,13 +617,19 @@ __device__ __forceinline__ void sym_work(const NsArgs& a, uint16_t* lds, int v) 
   }
   const int64_t pstride = int64_t(a.mp) * PANEL;
   const int r0 = ti * BM, c0 = tc * BN;
+  // on a diagonal tile the waves below the diagonal leave their sub-tile to
+  // the mirror of the one above it
+  const bool diag = tc == ti;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool skip = diag && below_diag(wave / NWN, wave % NWN);
   f32x16 acc[TMI][TMJ];
   if (STAGE == NS_SYRK)
-    mainloop<OP_K, OP_K>(src + r0 * PANEL, nullptr, 0, src + c0 * PANEL, nullptr, 0, pstride, K / BK, lds, acc);
+    mainloop<OP_K, OP_K>(src + r0 * PANEL, nullptr, 0, src + c0 * PANEL, nullptr, 0, pstride, K / BK, lds, acc,
+                         0.f, 0, skip);
   else  // acc = A A + (b/c) A, so P = c acc = b A + c A A
     mainloop<OP_SPLIT, OP_SPLIT, IDENT_COL>(src + r0 * PANEL, src + (r0 / PANEL) * pstride, r0 / BK,
                                             src + c0 * PANEL, src + (c0 / PANEL) * pstride, c0 / BK,
-                                            pstride, K / BK, lds, acc, a.cb / a.cc, c0);
+                                            pstride, K / BK, lds, acc, a.cb / a.cc, c0, skip);
 
   float f = STAGE == NS_POLY ? a.cc : 1.f;  // SYRK: s^2 on the first iteration
   if (STAGE == NS_SYRK && a.scale != nullptr) {
@@ -587,9 +639,9 @@ __device__ __forceinline__ void sym_work(const NsArgs& a, uint16_t* lds, int v) 
   uint16_t* out = static_cast<uint16_t*>(a.out) + int64_t(b) * a.mp * a.mp;
   char* stage = reinterpret_cast<char*>(lds);
   barrier();  // every wave is done with the ring
-  stage_tile(stage, acc, f);
+  stage_tile(stage, acc, f, diag);
   barrier();
-  if (tc != ti) {
+  if (!diag) {
     // upper tile C[r0 + i][c0 + r] = T[r][i]
     uint16_t* dst = out + (c0 / PANEL) * pstride + int64_t(r0) * PANEL;
     stage_cols(stage, [&](int i, int r, const uint4& u) {
