@@ -215,9 +215,22 @@ enum { M_KK = 0, M_KT = 1, M_TT = 2 };        // forms of one slice pair (row, c
 constexpr bool row_t(int m) { return m == M_TT; }
 constexpr bool col_t(int m) { return m != M_KK; }
 
-template <int RK, int CK, int IDENT>
+// MASK: the wave's 32x32 MFMA tiles (bit i*TMJ + j) that are computed; the
+// others, and the fragment reads only they need, are left out.
+template <int RK, int CK, int IDENT, int MASK = 0xFF>
 struct Pipe {
   static_assert(RDMA == 2 && CDMA == 2, "two direct loads per thread and operand slice");
+  static constexpr bool tile_on(int i, int j) { return (MASK >> (i * TMJ + j)) & 1; }
+  // fragment read G (column fragments first, then row fragments) feeds a computed tile
+  static constexpr bool frag_on(int G) {
+    bool on = false;
+    if (G < TMJ) {
+      for (int i = 0; i < TMI; ++i) on = on || tile_on(i, G);
+    } else {
+      for (int j = 0; j < TMJ; ++j) on = on || tile_on(G - TMJ, j);
+    }
+    return on;
+  }
   static_assert(RK != OP_T && (RK == OP_K || CK != OP_K), "row T only where the column is T");
   // the last run of slices: column T throughout (PX), else both K
   static constexpr int ML = CK == OP_T ? M_KT : M_KK;
@@ -283,12 +296,12 @@ struct Pipe {
   }
   template <int KK, int M>
   __device__ __forceinline__ void load(int kt, Frags& f) const {
-    load_one<KK, 0, M>(kt, f);
-    load_one<KK, 1, M>(kt, f);
-    load_one<KK, 2, M>(kt, f);
-    load_one<KK, 3, M>(kt, f);
-    load_one<KK, 4, M>(kt, f);
-    load_one<KK, 5, M>(kt, f);
+    if constexpr (frag_on(0)) load_one<KK, 0, M>(kt, f);
+    if constexpr (frag_on(1)) load_one<KK, 1, M>(kt, f);
+    if constexpr (frag_on(2)) load_one<KK, 2, M>(kt, f);
+    if constexpr (frag_on(3)) load_one<KK, 3, M>(kt, f);
+    if constexpr (frag_on(4)) load_one<KK, 4, M>(kt, f);
+    if constexpr (frag_on(5)) load_one<KK, 5, M>(kt, f);
   }
 
   // Identity term of slice kt, which crosses this wave's identity at tile F.
@@ -312,6 +325,7 @@ struct Pipe {
       for (int j = 0; j < TMJ; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
+          if (!tile_on(F, j)) continue;
           const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (lds_i16x4*)(sc + (wn * TMJ + j) * 2048 + q * 8 * 64 + base));
 #pragma unroll
@@ -323,6 +337,7 @@ struct Pipe {
       for (int i = 0; i < TMI; ++i)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
+          if (!tile_on(i, F)) continue;
           const int rb = wm * WM + 32 * i + 8 * q + 4 * (g >> 1);  // first of the four rows
           const uint32_t off = uint32_t((rb + (l16 >> 2)) * 64 + (((k16 >> 3) ^ ((rb >> 2) & 3)) << 4) + (k16 & 7) * 2);
           const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sr + off));
@@ -343,10 +358,12 @@ struct Pipe {
   template <int M, int MN, int F>
   __device__ __forceinline__ void body(int kt, Frags& fa, Frags& fb, f32x16 (&acc)[TMI][TMJ]) const {
     static_assert(TMI * TMJ == 8 && SLICE_DMA <= 8 && TMI + TMJ <= 8, "one read / direct load per MFMA");
-#define MMUON_MFMA(f, g) acc[(g) / TMJ][(g) % TMJ] = mfma(f.r[(g) / TMJ], f.c[(g) % TMJ], acc[(g) / TMJ][(g) % TMJ]);
-#define MMUON_STEP0(g)                                            \
-    MMUON_MFMA(fa, g)                                             \
-    if constexpr ((g) < TMI + TMJ) load_one<1, (g), M>(kt, fb);   \
+#define MMUON_MFMA(f, g)                                                                          \
+    if constexpr (tile_on((g) / TMJ, (g) % TMJ))                                                  \
+      acc[(g) / TMJ][(g) % TMJ] = mfma(f.r[(g) / TMJ], f.c[(g) % TMJ], acc[(g) / TMJ][(g) % TMJ]);
+#define MMUON_STEP0(g)                                                           \
+    MMUON_MFMA(fa, g)                                                            \
+    if constexpr ((g) < TMI + TMJ && frag_on(g)) load_one<1, (g), M>(kt, fb);    \
     __builtin_amdgcn_sched_barrier(0);
     MMUON_STEP0(0) MMUON_STEP0(1) MMUON_STEP0(2) MMUON_STEP0(3)
     MMUON_STEP0(4) MMUON_STEP0(5) MMUON_STEP0(6) MMUON_STEP0(7)
@@ -358,10 +375,10 @@ struct Pipe {
     // step has the same shape
     const int src = kt + NSTAGE - 1 < KT ? kt + NSTAGE - 1 : KT - 1;
     const int slot = kt + NSTAGE - 1;
-#define MMUON_STEP1(g)                                              \
-    MMUON_MFMA(fb, g)                                               \
-    if constexpr ((g) < TMI + TMJ) load_one<0, (g), MN>(kt + 1, fa); \
-    if constexpr ((g) < SLICE_DMA) issue_one<(g)>(src, slot);       \
+#define MMUON_STEP1(g)                                                               \
+    MMUON_MFMA(fb, g)                                                                \
+    if constexpr ((g) < TMI + TMJ && frag_on(g)) load_one<0, (g), MN>(kt + 1, fa);   \
+    if constexpr ((g) < SLICE_DMA) issue_one<(g)>(src, slot);                        \
     __builtin_amdgcn_sched_barrier(0);
     MMUON_STEP1(0) MMUON_STEP1(1) MMUON_STEP1(2) MMUON_STEP1(3)
     MMUON_STEP1(4) MMUON_STEP1(5) MMUON_STEP1(6) MMUON_STEP1(7)
@@ -447,17 +464,41 @@ struct Pipe {
   }
 };
 
-// Operand sources: *_k the K form (panel 0 at the operand's first row), *_t the
-// T form (row 0 of the first panel holding the operand's rows); thr_*: slices
-// kt < thr are T (OP_SPLIT); pstride: elements per panel.  ident_v: the identity
-// scalar; diag: K index of the tile's first row (IDENT_ROW) or column (IDENT_COL);
-// skip (wave-uniform): this wave only issues its share of the direct loads.
-template <int RK, int CK, int IDENT = IDENT_NONE>
-__device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t* rsrc_t, int thr_r,
-                                         const uint16_t* csrc_k, const uint16_t* csrc_t, int thr_c,
-                                         int64_t pstride, int KT, uint16_t* lds, f32x16 (&acc)[TMI][TMJ],
-                                         float ident_v = 0.f, int diag = 0, bool skip = false) {
-  Pipe<RK, CK, IDENT> p;
+// Roles of the waves in a diagonal tile of a symmetric product.  A 128 x 64
+// sub-tile strictly below the tile's diagonal is the transpose of one above it
+// (its wave only issues its direct loads); a sub-tile that starts on the
+// diagonal computes only its 32 x 32 tiles on or above it (MASK_DIAG).
+enum { WAVE_FULL = 0, WAVE_DIAG = 1, WAVE_IDLE = 2 };
+__device__ __forceinline__ bool below_diag(int wm, int wn) { return (wn + 1) * WN <= wm * WM; }
+__device__ __forceinline__ bool on_diag(int wm, int wn) { return wn * WN == wm * WM; }
+constexpr int mask_diag() {
+  int m = 0;
+  for (int i = 0; i < TMI; ++i)
+    for (int j = 0; j < TMJ; ++j)
+      if (j >= i) m |= 1 << (i * TMJ + j);
+  return m;
+}
+constexpr int MASK_DIAG = mask_diag();
+static_assert(WM == 2 * WN && BM == 2 * WM, "sub-tiles below the diagonal mirror sub-tiles above it");
+
+// 32 x 32 tile (R, C) of a diagonal tile (units of 32 rows / columns) is
+// computed by the wave that owns it.
+__device__ __forceinline__ bool diag_tile_computed(int R, int C) {
+  const int wm = R / (WM / 32), wn = C / (WN / 32);
+  if (below_diag(wm, wn)) return false;
+  return !on_diag(wm, wn) || C >= R;
+}
+__device__ __forceinline__ int diag_wave_role(int wave) {
+  const int wm = wave / NWN, wn = wave % NWN;
+  return below_diag(wm, wn) ? WAVE_IDLE : (on_diag(wm, wn) ? WAVE_DIAG : WAVE_FULL);
+}
+
+template <int RK, int CK, int IDENT, int MASK>
+__device__ __forceinline__ void mainloop_run(const uint16_t* rsrc_k, const uint16_t* rsrc_t, int thr_r,
+                                             const uint16_t* csrc_k, const uint16_t* csrc_t, int thr_c,
+                                             int64_t pstride, int KT, uint16_t* lds, f32x16 (&acc)[TMI][TMJ],
+                                             float ident_v, int diag, bool loads_only) {
+  Pipe<RK, CK, IDENT, MASK> p;
   p.rsrc_k = rsrc_k;
   p.rsrc_t = rsrc_t;
   p.csrc_k = csrc_k;
@@ -479,8 +520,26 @@ __device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t*
   p.tfrag_c = rowmajor_frag_base(p.wn * TMJ, p.lane);
   p.diag0 = diag + (IDENT == IDENT_ROW ? p.wm * WM : p.wn * WN);
   p.id_v = ident_v;
-  if (skip) p.run_loads_only(acc);
+  if (loads_only) p.run_loads_only(acc);
   else p.run(acc);
+}
+
+// Operand sources: *_k the K form (panel 0 at the operand's first row), *_t the
+// T form (row 0 of the first panel holding the operand's rows); thr_*: slices
+// kt < thr are T (OP_SPLIT); pstride: elements per panel.  ident_v: the identity
+// scalar; diag: K index of the tile's first row (IDENT_ROW) or column (IDENT_COL);
+// role (wave-uniform): WAVE_FULL, or this wave's role in a diagonal tile.
+template <int RK, int CK, int IDENT = IDENT_NONE>
+__device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t* rsrc_t, int thr_r,
+                                         const uint16_t* csrc_k, const uint16_t* csrc_t, int thr_c,
+                                         int64_t pstride, int KT, uint16_t* lds, f32x16 (&acc)[TMI][TMJ],
+                                         float ident_v = 0.f, int diag = 0, int role = WAVE_FULL) {
+  if (role == WAVE_DIAG)
+    mainloop_run<RK, CK, IDENT, MASK_DIAG>(rsrc_k, rsrc_t, thr_r, csrc_k, csrc_t, thr_c, pstride, KT, lds, acc,
+                                           ident_v, diag, false);
+  else
+    mainloop_run<RK, CK, IDENT, 0xFF>(rsrc_k, rsrc_t, thr_r, csrc_k, csrc_t, thr_c, pstride, KT, lds, acc,
+                                      ident_v, diag, role == WAVE_IDLE);
 }
 
 // ---------------------------------------------------------------------------
@@ -497,41 +556,22 @@ __device__ __forceinline__ uint32_t tile_off(int r, int c) {
   return uint32_t(r * 512 + ((((c >> 3) ^ g)) << 4) | ((c & 7) << 1));
 }
 
-// Waves of a diagonal tile of a symmetric product: a sub-tile strictly below
-// the tile's diagonal is the transpose of one strictly above it.
-__device__ __forceinline__ bool below_diag(int wm, int wn) { return (wn + 1) * WN <= wm * WM; }
-__device__ __forceinline__ bool above_diag(int wm, int wn) { return wn * WN >= (wm + 1) * WM; }
-static_assert(WM == 2 * WN && BM == 2 * WM, "the sub-tiles below the diagonal mirror those above it");
-
 // D[i][j] accumulators of this wave -> T[j][i] in the staging area, each value
 // scaled by f before the bf16 rounding.  Lane geometry: the lane holds column
 // j = 64 wn + 32 tj + lane%32 and rows i = 128 wm + 32 ti + 8 qg + 4 (lane/32) + e.
-// diag: a diagonal tile of a symmetric product whose waves below the diagonal
-// computed nothing; the waves above it also write T[i][j] = D[i][j] there.
+// diag: a diagonal tile of a symmetric product; its 32 x 32 tiles that were not
+// computed are filled from their transposes, T[i][j] = D[i][j].
 __device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI][TMJ], float f,
                                            bool diag = false) {
   const int tid = fresh_tid();
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / NWN, wn = wave % NWN;
-  if (diag && below_diag(wm, wn)) return;
-  if (diag && above_diag(wm, wn)) {
-#pragma unroll
-    for (int i = 0; i < TMI; ++i)
-#pragma unroll
-      for (int j = 0; j < TMJ; ++j)
-#pragma unroll
-        for (int qg = 0; qg < 4; ++qg)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int row = wm * WM + i * 32 + qg * 8 + (lane >> 5) * 4 + e;
-            const int col = wn * WN + j * 32 + (lane & 31);
-            *reinterpret_cast<uint16_t*>(stage + tile_off(row, col)) = f2bf(f * acc[i][j][qg * 4 + e]);
-          }
-  }
 #pragma unroll
   for (int i = 0; i < TMI; ++i) {
 #pragma unroll
     for (int j = 0; j < TMJ; ++j) {
+      const int R = wm * (WM / 32) + i, C = wn * (WN / 32) + j;
+      if (diag && !diag_tile_computed(R, C)) continue;
 #pragma unroll
       for (int qg = 0; qg < 4; ++qg) {
         float v[4];
@@ -540,6 +580,16 @@ __device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI]
         const int row = wn * WN + j * 32 + (lane & 31);
         const int col = wm * WM + i * 32 + qg * 8 + (lane >> 5) * 4;
         *reinterpret_cast<uint2*>(stage + tile_off(row, col)) = make_uint2(f2bf2(v[0], v[1]), f2bf2(v[2], v[3]));
+      }
+      if (diag && C > R && !diag_tile_computed(C, R)) {
+#pragma unroll
+        for (int qg = 0; qg < 4; ++qg)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int row = wm * WM + i * 32 + qg * 8 + (lane >> 5) * 4 + e;
+            const int col = wn * WN + j * 32 + (lane & 31);
+            *reinterpret_cast<uint16_t*>(stage + tile_off(row, col)) = f2bf(f * acc[i][j][qg * 4 + e]);
+          }
       }
     }
   }
@@ -617,19 +667,18 @@ __device__ __forceinline__ void sym_work(const NsArgs& a, uint16_t* lds, int v) 
   }
   const int64_t pstride = int64_t(a.mp) * PANEL;
   const int r0 = ti * BM, c0 = tc * BN;
-  // on a diagonal tile the waves below the diagonal leave their sub-tile to
-  // the mirror of the one above it
+  // on a diagonal tile only the 32 x 32 tiles on or above the diagonal are
+  // computed; the others are staged from their transposes
   const bool diag = tc == ti;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const bool skip = diag && below_diag(wave / NWN, wave % NWN);
+  const int role = diag ? diag_wave_role(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) : WAVE_FULL;
   f32x16 acc[TMI][TMJ];
   if (STAGE == NS_SYRK)
     mainloop<OP_K, OP_K>(src + r0 * PANEL, nullptr, 0, src + c0 * PANEL, nullptr, 0, pstride, K / BK, lds, acc,
-                         0.f, 0, skip);
+                         0.f, 0, role);
   else  // acc = A A + (b/c) A, so P = c acc = b A + c A A
     mainloop<OP_SPLIT, OP_SPLIT, IDENT_COL>(src + r0 * PANEL, src + (r0 / PANEL) * pstride, r0 / BK,
                                             src + c0 * PANEL, src + (c0 / PANEL) * pstride, c0 / BK,
-                                            pstride, K / BK, lds, acc, a.cb / a.cc, c0, skip);
+                                            pstride, K / BK, lds, acc, a.cb / a.cc, c0, role);
 
   float f = STAGE == NS_POLY ? a.cc : 1.f;  // SYRK: s^2 on the first iteration
   if (STAGE == NS_SYRK && a.scale != nullptr) {
