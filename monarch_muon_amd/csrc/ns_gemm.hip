@@ -622,10 +622,11 @@ __device__ __forceinline__ void stage_rows(const char* stage, uint16_t* dst, int
 template <class Fn>
 __device__ __forceinline__ void stage_cols(const char* stage, Fn&& fn) {
   const int tid = fresh_tid();
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, grp = lane >> 4;
 #pragma unroll 2
-  for (int task = wave; task < 16 * (BN / 32); task += NWAVES) {
+  for (int it = 0; it < 16 * (BN / 32) / NWAVES; ++it) {
+    const int task = wave + NWAVES * it;
     const int i0 = (task & 15) * 16, r0 = (task >> 4) * 32 + grp * 8;
     const int tr = r0 + (l16 >> 2), tc = i0 + ((l16 & 3) << 2);
     const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(stage + tile_off(tr, tc)));
@@ -775,6 +776,45 @@ __device__ __forceinline__ void px_work(const NsArgs& a, uint16_t* lds, int v) {
 
   const float s = a.scale != nullptr ? a.scale[b] : 1.f;
   char* stage = reinterpret_cast<char*>(lds);
+  // apply: param += alpha * u; the parameter block is stored (m x n)
+  // untransposed or (n x m) for a tall block
+  auto* prm = STAGE == NS_PX_APPLY ? reinterpret_cast<typename TP::storage*>(a.blocks[b].param) : nullptr;
+  const int m = a.m, n = a.n;
+  // 16-B vector access: aligned blocks and a row length that keeps chunks aligned
+  const bool vec = a.vec && ((TRANS ? m : n) % 8 == 0);
+  // bf16 parameters, tile inside the block: every parameter chunk of this
+  // thread is loaded in batches ahead of its use (the first batch before the
+  // tile is staged), then combined and stored
+  constexpr bool BF16P = sizeof(typename TP::storage) == 2;
+  const bool fast = STAGE == NS_PX_APPLY && BF16P && vec && r0 + BM <= m && c0 + BN <= n;
+  constexpr int CH = BN * BM / 8 / NT;  // 16-B chunks per thread
+  constexpr int BATCH = 8;
+  const int tid = fresh_tid();
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, grp = lane >> 4;
+  // chunk q of this thread: parameter offset, staged row r and column c of
+  // its first element (TRANS: 8 consecutive staged columns; else 8 staged rows)
+  auto chunk = [&](int q, int& r, int& c) -> int64_t {
+    if (TRANS) {
+      r = q * (NT / 32) + (tid >> 5);
+      c = (tid & 31) * 8;
+      return int64_t(c0 + r) * m + r0 + c;
+    }
+    const int task = wave + NWAVES * q;  // the stage_cols mapping
+    c = (task & 15) * 16;                // i0
+    r = (task >> 4) * 32 + grp * 8;
+    return int64_t(r0 + c + l16) * n + c0 + r;
+  };
+  uint4 pv[BATCH];
+  if constexpr (STAGE == NS_PX_APPLY && BF16P) {
+    if (fast) {
+#pragma unroll
+      for (int q = 0; q < BATCH; ++q) {
+        int r, c;
+        pv[q] = *reinterpret_cast<const uint4*>(prm + chunk(q, r, c));
+      }
+    }
+  }
   barrier();  // every wave is done with the ring
   stage_tile(stage, acc, s);
   barrier();
@@ -787,42 +827,17 @@ __device__ __forceinline__ void px_work(const NsArgs& a, uint16_t* lds, int v) {
     });
     return;
   }
-  // apply: param += alpha * u; the parameter block is stored (m x n)
-  // untransposed or (n x m) for a tall block
-  auto* prm = reinterpret_cast<typename TP::storage*>(a.blocks[b].param);
   const float alpha = a.alpha;
-  const int m = a.m, n = a.n;
-  // 16-B vector access: aligned blocks and a row length that keeps chunks aligned
-  const bool vec = a.vec && ((TRANS ? m : n) % 8 == 0);
-  if constexpr (sizeof(typename TP::storage) == 2) {
-    // bf16 parameters, tile inside the block: load every parameter chunk of this
-    // thread first, so their latencies overlap, then combine and store
-    if (vec && r0 + BM <= m && c0 + BN <= n) {
-      constexpr int CH = BN * BM / 8 / NT;  // 16-B chunks per thread
-      constexpr int BATCH = 8;
-      const int tid = fresh_tid();
-      const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-      const int l16 = lane & 15, grp = lane >> 4;
-      // chunk q of this thread: parameter offset, staged row r and column c of
-      // its first element (TRANS: 8 consecutive staged columns; else 8 staged rows)
-      auto chunk = [&](int q, int& r, int& c) -> int64_t {
-        if (TRANS) {
-          r = q * (NT / 32) + (tid >> 5);
-          c = (tid & 31) * 8;
-          return int64_t(c0 + r) * m + r0 + c;
-        }
-        const int task = wave + NWAVES * q;  // the stage_cols mapping
-        c = (task & 15) * 16;                // i0
-        r = (task >> 4) * 32 + grp * 8;
-        return int64_t(r0 + c + l16) * n + c0 + r;
-      };
+  if constexpr (BF16P) {
+    if (fast) {
 #pragma unroll
       for (int q0 = 0; q0 < CH; q0 += BATCH) {
-        uint4 pv[BATCH];
+        if (q0 > 0) {
 #pragma unroll
-        for (int q = 0; q < BATCH; ++q) {
-          int r, c;
-          pv[q] = *reinterpret_cast<const uint4*>(prm + chunk(q0 + q, r, c));
+          for (int q = 0; q < BATCH; ++q) {
+            int r, c;
+            pv[q] = *reinterpret_cast<const uint4*>(prm + chunk(q0 + q, r, c));
+          }
         }
 #pragma unroll
         for (int q = 0; q < BATCH; ++q) {
@@ -855,7 +870,6 @@ __device__ __forceinline__ void px_work(const NsArgs& a, uint16_t* lds, int v) {
     }
   }
   if (TRANS) {
-    const int tid = threadIdx.x;
     const int c = (tid & 31) * 8;
     for (int q = 0; q < BN / (NT / 32); ++q) {
       const int r = q * (NT / 32) + (tid >> 5);  // staged row = X' column = parameter row
