@@ -59,7 +59,6 @@ struct Vec8<F32T> {
 constexpr int PACK_NT = 256;
 constexpr int PACK_ITERS = 4;
 constexpr int PACK_ELEMS = PACK_NT * 8 * PACK_ITERS;  // X elements per workgroup (row layout)
-constexpr int PACK_TILE = 64;                          // transposed layout: 64 x 64 tiles
 
 // rows <= cols: X[b][i][j] = buf[b][i][j], 8 elements per thread.
 // fp32 X: the padded [mp][np] extent is walked in row-major order.
@@ -153,64 +152,84 @@ __global__ __launch_bounds__(PACK_NT) void pack_rows_kernel(PackArgs a) {
   if (threadIdx.x == 0) a.partial[int64_t(b) * a.nparts + blockIdx.x] = tot;
 }
 
-// rows > cols: X[b][i][j] = buf[b][j][i], transposed through a 64x64 LDS tile.
+// rows > cols: X[b][i][j] = buf[b][j][i].  A workgroup owns 32 buf rows (one
+// 32-column panel of X) x 256 buf columns (256 X rows): phase 1 reads the 32
+// rows (every wave two contiguous 1 KiB fp32 row segments per load), updates
+// the momentum and stages the rounded values in LDS; phase 2 gives each thread
+// one X row of the panel (64 contiguous bytes for bf16 X), so the workgroup's
+// X writes are one contiguous 16 KiB run.
+constexpr int PCOL_ROWS = 32;   // buf rows per workgroup
+constexpr int PCOL_COLS = 256;  // buf columns per workgroup (= PACK_NT)
+static_assert(PCOL_COLS == PACK_NT, "one X row per thread in phase 2");
 template <class TG, class TB, class TX>
 __global__ __launch_bounds__(PACK_NT) void pack_cols_kernel(PackArgs a) {
-  __shared__ float tile[PACK_TILE][PACK_TILE + 1];
+  __shared__ float tile[PCOL_ROWS][PCOL_COLS + 4];
   __shared__ float red[PACK_NT / 64];
+  constexpr int CHUNKS = PCOL_ROWS * PCOL_COLS / 8 / PACK_NT;  // 8-element chunks per thread
   const int b = blockIdx.y;
-  const int tiles_j = a.np / PACK_TILE;
-  const int ti = blockIdx.x / tiles_j, tj = blockIdx.x % tiles_j;
-  const int i0 = ti * PACK_TILE, j0 = tj * PACK_TILE;  // X coordinates
+  const int tiles_i = (a.mp + PCOL_COLS - 1) / PCOL_COLS;  // the last one partial when mp % 256 != 0
+  const int tj = blockIdx.x / tiles_i, ti = blockIdx.x % tiles_i;
+  const int r0 = tj * PCOL_ROWS, c0 = ti * PCOL_COLS;  // buf rows (X columns), buf columns (X rows)
   const mmuon_block_ref ref = a.blocks[b];
   const auto* g = reinterpret_cast<const typename TG::storage*>(ref.grad);
   auto* buf = reinterpret_cast<typename TB::storage*>(ref.buf);
   auto* x = reinterpret_cast<typename TX::storage*>(a.x) + int64_t(b) * a.mp * a.np;
-  // phase 1: buf rows r = j0 + t/4, columns c = i0 + (t%4)*16 + [0,16)
-  {
-    const int jr = threadIdx.x >> 2, seg = (threadIdx.x & 3) * 16;
-    const int r = j0 + jr;  // buf row  (= X column)
+  float ss = 0.f;
+  // phase 1: chunk e = q * PACK_NT + t covers buf row r0 + e/32, columns c0 + 8 (e%32) + [0, 8)
+  if (a.vec && r0 + PCOL_ROWS <= a.n && c0 + PCOL_COLS <= a.m) {
+    float gv[CHUNKS][8], bv[CHUNKS][8];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int c = i0 + seg + h * 8;  // buf col (= X row)
+    for (int q = 0; q < CHUNKS; ++q) {
+      const int e = q * PACK_NT + threadIdx.x;
+      const int64_t s = int64_t(r0 + (e >> 5)) * a.m + c0 + (e & 31) * 8;
+      Vec8<TG>::load(g + s, gv[q]);
+      Vec8<TB>::load(buf + s, bv[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < CHUNKS; ++q) {
+      const int e = q * PACK_NT + threadIdx.x;
+      const int64_t s = int64_t(r0 + (e >> 5)) * a.m + c0 + (e & 31) * 8;
       float v[8];
-      if (a.vec && r < a.n && c + 8 <= a.m) {
-        const int64_t s = int64_t(r) * a.m + c;
-        float gv[8];
-        Vec8<TG>::load(g + s, gv);
-        Vec8<TB>::load(buf + s, v);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] = momentum_update<TB>(v[q], gv[q], a.mu);
-        Vec8<TB>::store(buf + s, v);
-      } else {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          v[q] = 0.f;
-          if (r < a.n && c + q < a.m) {
-            const int64_t s = int64_t(r) * a.m + c + q;
-            v[q] = momentum_update<TB>(TB::load(buf, s), TG::load(g, s), a.mu);
-            TB::store(buf, s, v[q]);
-          }
-        }
+      for (int k = 0; k < 8; ++k) {
+        bv[q][k] = momentum_update<TB>(bv[q][k], gv[q][k], a.mu);
+        v[k] = TX::round(bv[q][k]);
+        ss += v[k] * v[k];
       }
+      Vec8<TB>::store(buf + s, bv[q]);
+      float4* t4 = reinterpret_cast<float4*>(&tile[e >> 5][(e & 31) * 8]);
+      t4[0] = make_float4(v[0], v[1], v[2], v[3]);
+      t4[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+  } else {
 #pragma unroll
-      for (int q = 0; q < 8; ++q) tile[jr][seg + h * 8 + q] = TX::round(v[q]);
+    for (int q = 0; q < CHUNKS; ++q) {
+      const int e = q * PACK_NT + threadIdx.x;
+      const int r = r0 + (e >> 5), c = c0 + (e & 31) * 8;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        float v = 0.f;
+        if (r < a.n && c + k < a.m) {
+          const int64_t s = int64_t(r) * a.m + c + k;
+          const float nb = momentum_update<TB>(TB::load(buf, s), TG::load(g, s), a.mu);
+          TB::store(buf, s, nb);
+          v = TX::round(nb);
+        }
+        ss += v * v;
+        tile[e >> 5][(e & 31) * 8 + k] = v;
+      }
     }
   }
   __syncthreads();
-  // phase 2: X rows i = i0 + t/4, columns j = j0 + (t%4)*16 + [0,16)
-  float ss = 0.f;
-  {
-    const int ir = threadIdx.x >> 2, seg = (threadIdx.x & 3) * 16;
+  // phase 2: X row c0 + t, columns r0 .. r0+31 (zeros in the padding)
+  const int t = threadIdx.x;
+  if (c0 + t < a.mp) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < PCOL_ROWS / 8; ++h) {
       float v[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        v[q] = tile[seg + h * 8 + q][ir];
-        ss += v[q] * v[q];
-      }
-      Vec8<TX>::store(x + TX::xoff(a.mp, a.np, i0 + ir, j0 + seg + h * 8), v);
+      for (int k = 0; k < 8; ++k) v[k] = tile[h * 8 + k][t];
+      Vec8<TX>::store(x + TX::xoff(a.mp, a.np, c0 + t, r0 + h * 8), v);
     }
   }
   const float tot = block_sum<PACK_NT>(ss, red);
@@ -218,7 +237,7 @@ __global__ __launch_bounds__(PACK_NT) void pack_cols_kernel(PackArgs a) {
 }
 
 int pack_nparts(int mp, int np_, bool transposed) {
-  if (transposed) return (mp / PACK_TILE) * (np_ / PACK_TILE);
+  if (transposed) return ((mp + PCOL_COLS - 1) / PCOL_COLS) * (np_ / PCOL_ROWS);
   const int64_t total = int64_t(mp) * np_;
   return int((total + PACK_ELEMS - 1) / PACK_ELEMS);
 }
