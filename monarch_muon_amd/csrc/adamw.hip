@@ -40,7 +40,41 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_kernel(AdamWArgs a) {
   const auto* g = reinterpret_cast<const typename TG::storage*>(T.grad);
   auto* m = reinterpret_cast<typename TS::storage*>(T.exp_avg);
   auto* v = reinterpret_cast<typename TS::storage*>(T.exp_avg_sq);
-  for (int64_t i = start + threadIdx.x; i < end; i += ADAM_NT) {
+  int64_t tail = start;
+  // 8 elements per thread and 16-B accesses when all four streams are aligned
+  // here; two groups' loads are issued before either is computed
+  const uintptr_t al = reinterpret_cast<uintptr_t>(p + start) | reinterpret_cast<uintptr_t>(g + start) |
+                       reinterpret_cast<uintptr_t>(m + start) | reinterpret_cast<uintptr_t>(v + start);
+  if ((al & 15) == 0) {
+    const int64_t stop = start + ((end - start) & ~int64_t(7));
+    for (int64_t i0 = start + int64_t(threadIdx.x) * 8; i0 < stop; i0 += 2 * ADAM_NT * 8) {
+      const int64_t i1 = i0 + ADAM_NT * 8;
+      const bool two = i1 < stop;
+      float P[2][8], G[2][8], M[2][8], V[2][8];
+      Vec8<TP>::load(p + i0, P[0]);
+      Vec8<TG>::load(g + i0, G[0]);
+      Vec8<TS>::load(m + i0, M[0]);
+      Vec8<TS>::load(v + i0, V[0]);
+      if (two) {
+        Vec8<TP>::load(p + i1, P[1]);
+        Vec8<TG>::load(g + i1, G[1]);
+        Vec8<TS>::load(m + i1, M[1]);
+        Vec8<TS>::load(v + i1, V[1]);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (h == 1 && !two) break;
+        const int64_t i = h ? i1 : i0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) adamw_elem<TP, TS>(P[h][e], G[h][e], M[h][e], V[h][e], a);
+        Vec8<TP>::store(p + i, P[h]);
+        Vec8<TS>::store(m + i, M[h]);
+        Vec8<TS>::store(v + i, V[h]);
+      }
+    }
+    tail = stop;
+  }
+  for (int64_t i = tail + threadIdx.x; i < end; i += ADAM_NT) {
     float pv = TP::load(p, i), mv = TS::load(m, i), vv = TS::load(v, i);
     adamw_elem<TP, TS>(pv, TG::load(g, i), mv, vv, a);
     TP::store(p, i, pv);

@@ -19,43 +19,6 @@ __device__ __forceinline__ float momentum_update(float buf, float g, float mu) {
   return TB::round(t + g);
 }
 
-// 8 consecutive elements, vector access (16-B aligned for bf16, 32 B for fp32)
-template <class T>
-struct Vec8;
-template <>
-struct Vec8<BF16T> {
-  static __device__ __forceinline__ void load(const uint16_t* p, float v[8]) {
-    const uint4 r = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      v[2 * q] = __uint_as_float(w[q] << 16);
-      v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
-    }
-  }
-  static __device__ __forceinline__ void store(uint16_t* p, const float v[8]) {
-    uint4 r;
-    r.x = uint32_t(f2bf(v[0])) | (uint32_t(f2bf(v[1])) << 16);
-    r.y = uint32_t(f2bf(v[2])) | (uint32_t(f2bf(v[3])) << 16);
-    r.z = uint32_t(f2bf(v[4])) | (uint32_t(f2bf(v[5])) << 16);
-    r.w = uint32_t(f2bf(v[6])) | (uint32_t(f2bf(v[7])) << 16);
-    *reinterpret_cast<uint4*>(p) = r;
-  }
-};
-template <>
-struct Vec8<F32T> {
-  static __device__ __forceinline__ void load(const float* p, float v[8]) {
-    const float4 a = reinterpret_cast<const float4*>(p)[0];
-    const float4 b = reinterpret_cast<const float4*>(p)[1];
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-  }
-  static __device__ __forceinline__ void store(float* p, const float v[8]) {
-    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
-    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
-  }
-};
-
 constexpr int PACK_NT = 256;
 constexpr int PACK_ITERS = 4;
 constexpr int PACK_ELEMS = PACK_NT * 8 * PACK_ITERS;  // X elements per workgroup (row layout)
