@@ -101,16 +101,47 @@ int launch_adamw(const AdamWArgs& a, int param_dtype, int grad_dtype, int state_
 }
 
 // ---------------------------------------------------------------------------
-// FP8-state AdamW: one wave per 128-element metadata group; the moments are
-// dequantized to fp32, updated in fp32 (the reference's dequantized states are
-// fp32 tensors), and requantized (exp_avg signed, exp_avg_sq unsigned).
+// FP8-state AdamW: one 128-element metadata group per 16-lane row, 8
+// consecutive elements per lane; the moments are dequantized to fp32, updated
+// in fp32 (the reference's dequantized states are fp32 tensors), and
+// requantized (exp_avg signed, exp_avg_sq unsigned).
 // chunk = tensor << 40 | first element of the group.
 // ---------------------------------------------------------------------------
+constexpr int F8_GPW = ADAM_NT / 16;  // groups per workgroup
+
+template <class T>
+__device__ __forceinline__ void load8_masked(const typename T::storage* p, int64_t e0, int nvalid, bool vec,
+                                             float v[8]) {
+  if (vec) {
+    Vec8<T>::load(p + e0, v);
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = k < nvalid ? T::load(p, e0 + k) : 0.f;
+}
+__device__ __forceinline__ uint2 load_codes(const uint8_t* q, int64_t e0, int nvalid, bool vec) {
+  if (vec) return *reinterpret_cast<const uint2*>(q + e0);
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (k < nvalid) w[k >> 2] |= uint32_t(q[e0 + k]) << (8 * (k & 3));
+  return make_uint2(w[0], w[1]);
+}
+__device__ __forceinline__ void store_codes(uint8_t* q, int64_t e0, int nvalid, bool vec, uint2 c) {
+  if (vec) {
+    *reinterpret_cast<uint2*>(q + e0) = c;
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (k < nvalid) q[e0 + k] = uint8_t((k < 4 ? c.x : c.y) >> (8 * (k & 3)));
+}
+
 template <class TP, class TG>
 __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
-  const int64_t gidx = int64_t(blockIdx.x) * (ADAM_NT / 64) + (threadIdx.x >> 6);
-  if (gidx >= a.nchunks) return;
-  const int lane = threadIdx.x & 63;
+  const int64_t gidx = int64_t(blockIdx.x) * F8_GPW + (threadIdx.x >> 4);
+  if (gidx >= a.nchunks) return;  // whole 16-lane rows leave together
+  const int sub = threadIdx.x & 15;
   const int64_t code = a.chunks[gidx];
   const int t = int(code >> 40);
   const int64_t start = code & ((int64_t(1) << 40) - 1);
@@ -121,36 +152,36 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
   const auto* g = reinterpret_cast<const typename TG::storage*>(T.grad);
   uint8_t* qm = reinterpret_cast<uint8_t*>(T.exp_avg);
   uint8_t* qv = reinterpret_cast<uint8_t*>(T.exp_avg_sq);
-  Fp8Meta mm{0.f, 0.f, 0.f}, mv{0.f, 0.f, 0.f};
+  const int64_t e0 = start + sub * 8;
+  const int nvalid = int(max(int64_t(0), min(int64_t(8), T.numel - e0)));
+  // 16-B parameter / gradient and 8-B code accesses for a full, aligned lane
+  const uintptr_t al = reinterpret_cast<uintptr_t>(p + e0) | reinterpret_cast<uintptr_t>(g + e0);
+  const bool vec = nvalid == 8 && (al & 15) == 0 &&
+                   ((reinterpret_cast<uintptr_t>(qm + e0) | reinterpret_cast<uintptr_t>(qv + e0)) & 7) == 0;
+  float pv[8], gv[8], m[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  load8_masked<TP>(p, e0, nvalid, vec, pv);
+  load8_masked<TG>(g, e0, nvalid, vec, gv);
   if (a.have_state) {
-    mm = Fp8Meta{M.scale_m[grp], M.expand_m[grp], M.sqrt_minmax_m[grp]};
-    mv = Fp8Meta{M.scale_v[grp], M.expand_v[grp], M.sqrt_minmax_v[grp]};
+    fp8_dequant8(load_codes(qm, e0, nvalid, vec), fp8_dq(Fp8Meta{M.scale_m[grp], M.expand_m[grp], M.sqrt_minmax_m[grp]}),
+                 true, m);
+    fp8_dequant8(load_codes(qv, e0, nvalid, vec), fp8_dq(Fp8Meta{M.scale_v[grp], M.expand_v[grp], M.sqrt_minmax_v[grp]}),
+                 false, v);
   }
-  float mo[2], vo[2];
-  bool ok[2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int64_t i = start + lane + 64 * h;
-    ok[h] = i < T.numel;
-    mo[h] = vo[h] = 0.f;
-    if (ok[h]) {
-      float pv = TP::load(p, i);
-      float m = a.have_state ? fp8_dequant(qm[i], mm, true) : 0.f;
-      float v = a.have_state ? fp8_dequant(qv[i], mv, false) : 0.f;
-      adamw_elem<TP, F32T>(pv, TG::load(g, i), m, v, a);
-      TP::store(p, i, pv);
-      mo[h] = m;
-      vo[h] = v;
-    }
+  for (int k = 0; k < 8; ++k) adamw_elem<TP, F32T>(pv[k], gv[k], m[k], v[k], a);
+  if (vec) {
+    Vec8<TP>::store(p + e0, pv);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k < nvalid) TP::store(p, e0 + k, pv[k]);
   }
-  uint8_t c0, c1;
-  const Fp8Meta nm = fp8_quant_group(mo[0], mo[1], ok[0], ok[1], true, c0, c1);
-  if (ok[0]) qm[start + lane] = c0;
-  if (ok[1]) qm[start + lane + 64] = c1;
-  const Fp8Meta nv = fp8_quant_group(vo[0], vo[1], ok[0], ok[1], false, c0, c1);
-  if (ok[0]) qv[start + lane] = c0;
-  if (ok[1]) qv[start + lane + 64] = c1;
-  if (lane == 0) {
+  uint2 c;
+  const Fp8Meta nm = fp8_quant16(m, nvalid, true, c);
+  store_codes(qm, e0, nvalid, vec, c);
+  const Fp8Meta nv = fp8_quant16(v, nvalid, false, c);
+  store_codes(qv, e0, nvalid, vec, c);
+  if (sub == 0) {
     M.scale_m[grp] = nm.scale;
     M.expand_m[grp] = nm.expand;
     M.sqrt_minmax_m[grp] = nm.sqrt_minmax;
@@ -162,7 +193,7 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
 
 int launch_adamw_fp8(const AdamWArgs& a, int param_dtype, int grad_dtype, hipStream_t s) {
   if (a.nchunks <= 0) return 0;
-  const dim3 grid(unsigned((a.nchunks + 3) / 4)), block(ADAM_NT);
+  const dim3 grid(unsigned((a.nchunks + F8_GPW - 1) / F8_GPW)), block(ADAM_NT);
   if (param_dtype == MMUON_BF16 && grad_dtype == MMUON_BF16)
     hipLaunchKernelGGL((adamw_fp8_kernel<BF16T, BF16T>), grid, block, 0, s, a);
   else if (param_dtype == MMUON_F32 && grad_dtype == MMUON_F32)

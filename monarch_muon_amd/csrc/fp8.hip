@@ -8,21 +8,27 @@ namespace mmuon {
 
 constexpr int F8_NT = 256;  // 4 waves = 4 groups per workgroup
 
-// coat_state_muon.py:103-114: fp32 values -> codes + per-group metadata.
+// coat_state_muon.py:103-114: fp32 values -> codes + per-group metadata.  One
+// group of 128 per 16-lane row, 8 consecutive elements per lane.
 __global__ __launch_bounds__(F8_NT) void fp8_quantize_kernel(const float* v, uint8_t* q, float* sc,
                                                              float* ex, float* smm, int64_t numel,
                                                              int sgn) {
-  const int64_t grp = int64_t(blockIdx.x) * (F8_NT / 64) + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int64_t i0 = grp * 128 + lane, i1 = i0 + 64;
-  if (grp * 128 >= numel) return;
-  const bool v0 = i0 < numel, v1 = i1 < numel;
-  const float x0 = v0 ? v[i0] : 0.f, x1 = v1 ? v[i1] : 0.f;
-  uint8_t c0, c1;
-  const Fp8Meta md = fp8_quant_group(x0, x1, v0, v1, sgn != 0, c0, c1);
-  if (v0) q[i0] = c0;
-  if (v1) q[i1] = c1;
-  if (lane == 0) {
+  const int64_t grp = int64_t(blockIdx.x) * (F8_NT / 16) + (threadIdx.x >> 4);
+  if (grp * 128 >= numel) return;  // whole 16-lane rows leave together
+  const int sub = threadIdx.x & 15;
+  const int64_t e0 = grp * 128 + sub * 8;
+  const int nvalid = int(max(int64_t(0), min(int64_t(8), numel - e0)));
+  float x[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) x[k] = k < nvalid ? v[e0 + k] : 0.f;
+  uint2 c;
+  const Fp8Meta md = fp8_quant16(x, nvalid, sgn != 0, c);
+  const uint8_t b[8] = {uint8_t(c.x), uint8_t(c.x >> 8), uint8_t(c.x >> 16), uint8_t(c.x >> 24),
+                        uint8_t(c.y), uint8_t(c.y >> 8), uint8_t(c.y >> 16), uint8_t(c.y >> 24)};
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (k < nvalid) q[e0 + k] = b[k];
+  if (sub == 0) {
     sc[grp] = md.scale;
     ex[grp] = md.expand;
     smm[grp] = md.sqrt_minmax;
@@ -43,7 +49,8 @@ void launch_fp8_quantize(const float* v, uint8_t* q, float* sc, float* ex, float
                          int64_t numel, bool sgn, hipStream_t s) {
   const int64_t groups = (numel + 127) / 128;
   if (groups == 0) return;
-  hipLaunchKernelGGL(fp8_quantize_kernel, dim3(unsigned((groups + 3) / 4)), dim3(F8_NT), 0, s, v, q,
+  constexpr int GPW = F8_NT / 16;  // groups per workgroup
+  hipLaunchKernelGGL(fp8_quantize_kernel, dim3(unsigned((groups + GPW - 1) / GPW)), dim3(F8_NT), 0, s, v, q,
                      sc, ex, smm, numel, int(sgn));
 }
 
@@ -61,110 +68,130 @@ void launch_fp8_dequantize(const uint8_t* q, const float* sc, const float* ex, c
 // (coat_state_muon.py:126-139).  The momentum is not touched between its update
 // and the requantization, so both happen here in one pass.
 // ---------------------------------------------------------------------------
-template <class TG, class TX>
-__device__ __forceinline__ float fp8_momentum_elem(const uint8_t* q, const Fp8Meta& md, int64_t i,
-                                                   const typename TG::storage* g, float mu,
-                                                   int have_state) {
-  const float old = have_state ? fp8_dequant(q[i], md, true) : 0.f;
-  const float t = old * mu;
-  return t + TG::load(g, i);
+constexpr int F8_GPW = F8_NT / 16;  // 128-groups per workgroup: one per 16-lane row
+
+// This lane's 8 momentum values after the update: dequantized codes (zeros
+// without state) * mu + g, each op rounded to fp32 as the reference's fp32
+// foreach ops round.
+template <class TG>
+__device__ __forceinline__ void fp8_momentum8(const uint8_t* q, const float* scale, const float* expand,
+                                              const float* smm, int64_t grp, int64_t e0,
+                                              const typename TG::storage* g, float mu, int have_state,
+                                              float nv[8]) {
+  float old[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (have_state) {
+    const uint2 c = *reinterpret_cast<const uint2*>(q + e0);
+    fp8_dequant8(c, fp8_dq(Fp8Meta{scale[grp], expand[grp], smm[grp]}), true, old);
+  }
+  float gv[8];
+  Vec8<TG>::load(g + e0, gv);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float t = old[k] * mu;
+    nv[k] = t + gv[k];
+  }
 }
 
-// One wave per 128-group of a block (groups may wrap rows).  TRANS: the block
-// is tall (rows > cols) and X holds its transpose; the general fallback for
-// tall blocks whose width is not a multiple of 128 (scattered X stores).
+__device__ __forceinline__ void fp8_store_group(uint8_t* q, const mmuon_block_fp8& md, int64_t grp, int64_t e0,
+                                                const float nv[8]) {
+  uint2 c;
+  const Fp8Meta nm = fp8_quant16(nv, 8, true, c);
+  *reinterpret_cast<uint2*>(q + e0) = c;
+  if ((threadIdx.x & 15) == 0) {
+    md.scale[grp] = nm.scale;
+    md.expand[grp] = nm.expand;
+    md.sqrt_minmax[grp] = nm.sqrt_minmax;
+  }
+}
+
+// A 16-lane row per 128-group of a block (groups may wrap rows), 8 elements
+// per lane.  TRANS: the block is tall (rows > cols) and X holds its transpose;
+// the fallback for tall blocks whose width is not a multiple of 128 (scattered
+// X stores).
 template <class TG, class TX, bool TRANS>
 __global__ __launch_bounds__(F8_NT) void fp8_pack_rows_kernel(PackArgs a, const mmuon_block_fp8* meta,
                                                               int rows, int cols, int have_state) {
   __shared__ float red[F8_NT / 64];
   const int b = blockIdx.y;
-  const int lane = threadIdx.x & 63;
   const int64_t gpb = int64_t(rows) * cols / 128;  // groups per block
-  const int64_t grp = int64_t(blockIdx.x) * (F8_NT / 64) + (threadIdx.x >> 6);
+  const int64_t grp = int64_t(blockIdx.x) * F8_GPW + (threadIdx.x >> 4);
   const mmuon_block_ref ref = a.blocks[b];
   const mmuon_block_fp8 md = meta[b];
   const auto* g = reinterpret_cast<const typename TG::storage*>(ref.grad);
   uint8_t* q = reinterpret_cast<uint8_t*>(ref.buf);
   auto* x = reinterpret_cast<typename TX::storage*>(a.x) + int64_t(b) * a.mp * a.np;
   float ss = 0.f;
-  if (grp < gpb) {
-    Fp8Meta m0{0.f, 0.f, 0.f};
-    if (have_state) m0 = Fp8Meta{md.scale[grp], md.expand[grp], md.sqrt_minmax[grp]};
-    float nv[2];
+  if (grp < gpb) {  // uniform over the 16-lane row
+    const int64_t e0 = grp * 128 + (threadIdx.x & 15) * 8;
+    float nv[8];
+    fp8_momentum8<TG>(q, md.scale, md.expand, md.sqrt_minmax, grp, e0, g, a.mu, have_state, nv);
+    float xv[8];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int64_t e = grp * 128 + lane + 64 * h;
-      nv[h] = fp8_momentum_elem<TG, TX>(q, m0, e, g, a.mu, have_state);
-      const float xv = TX::round(nv[h]);
-      ss += xv * xv;
-      const int64_t r = e / cols, c = e % cols;
-      TX::store(x, TRANS ? TX::xoff(a.mp, a.np, c, r) : TX::xoff(a.mp, a.np, r, c), xv);
+    for (int k = 0; k < 8; ++k) {
+      xv[k] = TX::round(nv[k]);
+      ss += xv[k] * xv[k];
     }
-    uint8_t c0, c1;
-    const Fp8Meta nm = fp8_quant_group(nv[0], nv[1], true, true, true, c0, c1);
-    q[grp * 128 + lane] = c0;
-    q[grp * 128 + lane + 64] = c1;
-    if (lane == 0) {
-      md.scale[grp] = nm.scale;
-      md.expand[grp] = nm.expand;
-      md.sqrt_minmax[grp] = nm.sqrt_minmax;
+    if (!TRANS && cols % 8 == 0) {
+      Vec8<TX>::store(x + TX::xoff(a.mp, a.np, e0 / cols, e0 % cols), xv);  // 8 elements in one panel
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int64_t r = (e0 + k) / cols, c = (e0 + k) % cols;
+        TX::store(x, TRANS ? TX::xoff(a.mp, a.np, c, r) : TX::xoff(a.mp, a.np, r, c), xv[k]);
+      }
     }
+    fp8_store_group(q, md, grp, e0, nv);
   }
   const float tot = block_sum<F8_NT>(ss, red);
   if (threadIdx.x == 0) a.partial[int64_t(b) * a.nparts + blockIdx.x] = tot;
 }
 
-// rows > cols (cols % 128 == 0): a workgroup owns 64 block rows x 128 block
-// columns (64 groups, 16 per wave) and writes the transposed X tile through LDS.
+// rows > cols, cols % 128 == 0: a workgroup owns 32 block rows x 128 block
+// columns (32 groups, two per 16-lane row) and writes the transposed X tile
+// through LDS: X rows c0 .. c0+127, columns r0 .. r0+31 (32-B runs per thread).
+constexpr int F8T_ROWS = 32;
 template <class TG, class TX>
 __global__ __launch_bounds__(F8_NT) void fp8_pack_cols_kernel(PackArgs a, const mmuon_block_fp8* meta,
                                                               int rows, int cols, int have_state) {
-  __shared__ float tile[64][128 + 1];
+  __shared__ float tile[F8T_ROWS][128 + 4];
   __shared__ float red[F8_NT / 64];
   const int b = blockIdx.y;
   const int tiles_c = cols / 128;
-  const int r0 = (blockIdx.x / tiles_c) * 64, c0 = (blockIdx.x % tiles_c) * 128;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r0 = (blockIdx.x / tiles_c) * F8T_ROWS, c0 = (blockIdx.x % tiles_c) * 128;
+  const int sub = threadIdx.x & 15, row16 = threadIdx.x >> 4;
   const mmuon_block_ref ref = a.blocks[b];
   const mmuon_block_fp8 md = meta[b];
   const auto* g = reinterpret_cast<const typename TG::storage*>(ref.grad);
   uint8_t* q = reinterpret_cast<uint8_t*>(ref.buf);
   auto* x = reinterpret_cast<typename TX::storage*>(a.x) + int64_t(b) * a.mp * a.np;
-  for (int k = 0; k < 16; ++k) {
-    const int rl = wave * 16 + k, r = r0 + rl;
-    float nv[2] = {0.f, 0.f};
-    if (r < rows) {
-      const int64_t grp = (int64_t(r) * cols + c0) / 128;
-      Fp8Meta m0{0.f, 0.f, 0.f};
-      if (have_state) m0 = Fp8Meta{md.scale[grp], md.expand[grp], md.sqrt_minmax[grp]};
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int64_t e = int64_t(r) * cols + c0 + lane + 64 * h;
-        nv[h] = fp8_momentum_elem<TG, TX>(q, m0, e, g, a.mu, have_state);
-      }
-      uint8_t cA, cB;
-      const Fp8Meta nm = fp8_quant_group(nv[0], nv[1], true, true, true, cA, cB);
-      q[grp * 128 + lane] = cA;
-      q[grp * 128 + lane + 64] = cB;
-      if (lane == 0) {
-        md.scale[grp] = nm.scale;
-        md.expand[grp] = nm.expand;
-        md.sqrt_minmax[grp] = nm.sqrt_minmax;
-      }
+  for (int h = 0; h < F8T_ROWS / F8_GPW; ++h) {
+    const int rl = row16 + F8_GPW * h, r = r0 + rl;
+    float nv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (r < rows) {  // uniform over the 16-lane row
+      const int64_t e0 = int64_t(r) * cols + c0 + sub * 8;
+      const int64_t grp = e0 >> 7;
+      fp8_momentum8<TG>(q, md.scale, md.expand, md.sqrt_minmax, grp, e0, g, a.mu, have_state, nv);
+      fp8_store_group(q, md, grp, e0, nv);
     }
-    tile[rl][lane] = TX::round(nv[0]);
-    tile[rl][lane + 64] = TX::round(nv[1]);
+    float4* t4 = reinterpret_cast<float4*>(&tile[rl][sub * 8]);
+    t4[0] = make_float4(TX::round(nv[0]), TX::round(nv[1]), TX::round(nv[2]), TX::round(nv[3]));
+    t4[1] = make_float4(TX::round(nv[4]), TX::round(nv[5]), TX::round(nv[6]), TX::round(nv[7]));
   }
   __syncthreads();
-  // X[c][r0 .. r0+63] for c in [c0, c0+128): thread -> (c = t/2, 32 consecutive r)
+  // X row c0 + t/2, columns r0 + 16 (t%2) .. +15
   float ss = 0.f;
   {
-    const int cl = threadIdx.x >> 1, half = (threadIdx.x & 1) * 32;
-    for (int k = 0; k < 32; ++k) {
-      const int rl = half + k, r = r0 + rl;
-      const float v = tile[rl][cl];
-      ss += v * v;
-      if (r < a.np) TX::store(x, TX::xoff(a.mp, a.np, c0 + cl, r), v);
+    const int cl = threadIdx.x >> 1, half = (threadIdx.x & 1) * 16;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        v[k] = tile[half + h * 8 + k][cl];
+        ss += v[k] * v[k];
+      }
+      Vec8<TX>::store(x + TX::xoff(a.mp, a.np, c0 + cl, r0 + half + h * 8), v);
     }
   }
   const float tot = block_sum<F8_NT>(ss, red);
@@ -184,9 +211,9 @@ __global__ __launch_bounds__(256) void zero_pads_kernel(void* xv, int m, int n, 
 }
 
 int fp8_pack_nparts(int rows, int cols, bool transposed) {
-  if (transposed && cols % 128 == 0) return ((rows + 63) / 64) * (cols / 128);
+  if (transposed && cols % 128 == 0) return ((rows + F8T_ROWS - 1) / F8T_ROWS) * (cols / 128);
   const int64_t gpb = int64_t(rows) * cols / 128;
-  return int((gpb + 3) / 4);
+  return int((gpb + F8_GPW - 1) / F8_GPW);
 }
 
 int launch_fp8_pack(const PackArgs& a, const mmuon_block_fp8* meta, int rows, int cols,

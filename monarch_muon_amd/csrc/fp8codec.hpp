@@ -2,8 +2,8 @@
 //
 // Device restatement of the codec of coat_state_muon.py:22-91 (itself the
 // first/second-order half of COAT's AdamW expand kernel).  Each group of 128
-// consecutive elements carries fp32 scale, expand and sqrt_minmax.  One wave64
-// owns one group, two elements per lane (lane and lane+64).
+// consecutive elements carries fp32 scale, expand and sqrt_minmax.  A group is
+// held by a row of 16 lanes, 8 consecutive elements per lane.
 #pragma once
 
 #include "common.hpp"
@@ -14,30 +14,7 @@ constexpr float FP8_MAX = 448.0f;
 constexpr float QEPS = 1e-30f;
 constexpr float EXPAND_MIN = 16.0f;
 
-// fp32 -> e4m3fn byte: round to nearest even, saturating at +-448, NaN -> 0x7f.
-__device__ __forceinline__ uint8_t e4m3_encode(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  float a = fabsf(x);
-  if (a != a) return uint8_t(0x7fu | sign);
-  a = fminf(a, FP8_MAX);
-  if (a < 0.015625f) {                       // below 2^-6: multiples of 2^-9
-    const float k = rintf(a * 512.0f);       // exact scaling, RNE; k == 8 is the min normal
-    return uint8_t(sign | uint32_t(k));
-  }
-  const uint32_t au = __float_as_uint(a);
-  uint32_t e = (au >> 23) - 127u + 7u;
-  const uint32_t man = au & 0x7fffffu;
-  uint32_t q = man >> 20;
-  const uint32_t rem = man & 0xfffffu;
-  q += (rem > 0x80000u) || (rem == 0x80000u && (q & 1u));
-  if (q == 8u) {
-    q = 0u;
-    e += 1u;
-  }
-  return uint8_t(sign | (e << 3) | q);
-}
-
+// e4m3fn byte -> fp32 (exact).
 __device__ __forceinline__ float e4m3_decode(uint32_t c) {
   const uint32_t e = (c >> 3) & 0xfu, m = c & 7u;
   float v;
@@ -51,38 +28,121 @@ struct Fp8Meta {
   float scale, expand, sqrt_minmax;
 };
 
-// coat_state_muon.py:22-43 for one element.
-__device__ __forceinline__ float fp8_dequant(uint32_t code, const Fp8Meta& md, bool sgn) {
-  const float ex = fmaxf(md.expand, QEPS);
-  const float smm = fmaxf(md.sqrt_minmax, QEPS);
-  const float inv = 1.0f / ex;
-  const float raw = e4m3_decode(code);
-  if (sgn) {
-    const float scaled = raw * md.scale;
-    const float absolute = fabsf(scaled);
-    const float s = scaled >= 0.f ? 1.f : -1.f;
-    const float power = powf(fmaxf(absolute, QEPS), inv);
-    return absolute > 0.f ? (s * power) * smm : 0.f;
-  }
-  const float scaled = fmaxf(raw * md.scale, 0.f);
-  const float power = powf(fmaxf(scaled, QEPS), inv);
-  return scaled > 0.f ? power * smm : 0.f;
+// x^y for a positive normal x, as 2^(y log2 x) with the hardware base-2
+// logarithm and exponential (v_log_f32, v_exp_f32).  Rounding the product
+// y log2 x adds a relative error of about |y log2 x| * 2^-24 to the result; the
+// codec's per-element powers have |y log2 x| below ~20 for any group whose
+// values are not denormal-scale, so the result stays within ~1e-6 relative.
+__device__ __forceinline__ float pow_pos(float x, float y) {
+  return __builtin_amdgcn_exp2f(y * __builtin_amdgcn_logf(x));
 }
 
-// coat_state_muon.py:46-91 for one group held by a whole wave (two elements
-// per lane; v0/v1 say whether the element exists).  Returns the codes of this
-// lane's two elements and the group metadata (valid in every lane).
-__device__ __forceinline__ Fp8Meta fp8_quant_group(float x0, float x1, bool v0, bool v1, bool sgn,
-                                                   uint8_t& q0, uint8_t& q1) {
-  const float a0 = fabsf(x0), a1 = fabsf(x1);
-  float amax = fmaxf(v0 ? a0 : 0.f, v1 ? a1 : 0.f);
-  const bool n0 = v0 && a0 > 0.f, n1 = v1 && a1 > 0.f;
-  float amin = fminf(n0 ? a0 : 3.4028235e38f, n1 ? a1 : 3.4028235e38f);
-  const int nz = wave_isum(int(n0) + int(n1));
-  amax = wave_max(amax);
-  amin = wave_min(amin);
-  amax = fmaxf(amax, QEPS);
-  amin = nz > 0 ? fmaxf(amin, QEPS) : QEPS;
+// Per-group dequantization constants: scale, 1/expand, sqrt_minmax (clamped
+// as coat_state_muon.py:34-36 clamps them).
+struct Fp8Dq {
+  float scale, inv_expand, smm;
+};
+__device__ __forceinline__ Fp8Dq fp8_dq(const Fp8Meta& md) {
+  return Fp8Dq{md.scale, 1.0f / fmaxf(md.expand, QEPS), fmaxf(md.sqrt_minmax, QEPS)};
+}
+
+// coat_state_muon.py:22-43 for one element.
+__device__ __forceinline__ float fp8_dequant(uint32_t code, const Fp8Dq& d, bool sgn) {
+  const float raw = e4m3_decode(code);
+  if (sgn) {
+    const float scaled = raw * d.scale;
+    const float absolute = fabsf(scaled);
+    const float s = scaled >= 0.f ? 1.f : -1.f;
+    const float power = pow_pos(fmaxf(absolute, QEPS), d.inv_expand);
+    return absolute > 0.f ? (s * power) * d.smm : 0.f;
+  }
+  const float scaled = fmaxf(raw * d.scale, 0.f);
+  const float power = pow_pos(fmaxf(scaled, QEPS), d.inv_expand);
+  return scaled > 0.f ? power * d.smm : 0.f;
+}
+__device__ __forceinline__ float fp8_dequant(uint32_t code, const Fp8Meta& md, bool sgn) {
+  return fp8_dequant(code, fp8_dq(md), sgn);
+}
+
+// ---------------------------------------------------------------------------
+// Group of 128 held by 16 lanes, 8 consecutive elements per lane.
+// gfx950's v_cvt_f32_fp8 / v_cvt_pk_fp8_f32 convert OCP e4m3fn with
+// round-to-nearest-even (the rounding torch's float8_e4m3fn cast uses); the
+// encoder's inputs are clamped to +-448 first, as the codec saturates.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void e4m3_decode8(uint2 c, float v[8]) {
+  v[0] = __builtin_amdgcn_cvt_f32_fp8(int(c.x), 0);
+  v[1] = __builtin_amdgcn_cvt_f32_fp8(int(c.x), 1);
+  v[2] = __builtin_amdgcn_cvt_f32_fp8(int(c.x), 2);
+  v[3] = __builtin_amdgcn_cvt_f32_fp8(int(c.x), 3);
+  v[4] = __builtin_amdgcn_cvt_f32_fp8(int(c.y), 0);
+  v[5] = __builtin_amdgcn_cvt_f32_fp8(int(c.y), 1);
+  v[6] = __builtin_amdgcn_cvt_f32_fp8(int(c.y), 2);
+  v[7] = __builtin_amdgcn_cvt_f32_fp8(int(c.y), 3);
+}
+// values already clamped to [-448, 448]
+__device__ __forceinline__ uint2 e4m3_encode8(const float v[8]) {
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], lo, true);
+  int hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[4], v[5], 0, false);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(v[6], v[7], hi, true);
+  return make_uint2(uint32_t(lo), uint32_t(hi));
+}
+
+// Cross-lane max / min over a row of 16 lanes (every lane of the row active):
+// swap neighbours, swap pairs, mirror the halves of 8, mirror the row.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xb1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f<0x4e>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+  return fmaxf(v, dpp_f<0x140>(v));  // row_mirror
+}
+__device__ __forceinline__ float row16_min(float v) {
+  v = fminf(v, dpp_f<0xb1>(v));
+  v = fminf(v, dpp_f<0x4e>(v));
+  v = fminf(v, dpp_f<0x141>(v));
+  return fminf(v, dpp_f<0x140>(v));
+}
+
+__device__ __forceinline__ void fp8_dequant8(uint2 codes, const Fp8Dq& d, bool sgn, float out[8]) {
+  float raw[8];
+  e4m3_decode8(codes, raw);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (sgn) {
+      const float scaled = raw[k] * d.scale;
+      const float absolute = fabsf(scaled);
+      const float power = pow_pos(fmaxf(absolute, QEPS), d.inv_expand);
+      out[k] = absolute > 0.f ? copysignf(power, scaled) * d.smm : 0.f;
+    } else {
+      const float scaled = fmaxf(raw[k] * d.scale, 0.f);
+      const float power = pow_pos(fmaxf(scaled, QEPS), d.inv_expand);
+      out[k] = scaled > 0.f ? power * d.smm : 0.f;
+    }
+  }
+}
+
+// coat_state_muon.py:46-91 for one group held by 16 lanes (valid: this lane's
+// elements that exist).  Returns the group metadata (valid in every lane of the
+// row) and this lane's 8 codes.  The normalised value is multiplied by 1/scale
+// rather than divided by scale (one extra rounding, visible only at e4m3 ties).
+__device__ __forceinline__ Fp8Meta fp8_quant16(const float x[8], int nvalid, bool sgn, uint2& codes) {
+  float amax = 0.f, amin = 3.4028235e38f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float a = fabsf(x[k]);
+    if (k < nvalid) {
+      amax = fmaxf(amax, a);
+      if (a > 0.f) amin = fminf(amin, a);
+    }
+  }
+  amax = fmaxf(row16_max(amax), QEPS);
+  amin = row16_min(amin);
+  amin = amin < 3.4028235e38f ? fmaxf(amin, QEPS) : QEPS;  // no non-zero value: QEPS
   float ratio = amax / amin;
   ratio = fmaxf(ratio, 1.0f + QEPS);
   const float ratio_upper = FP8_MAX * FP8_MAX / 2.0f;
@@ -92,14 +152,17 @@ __device__ __forceinline__ Fp8Meta fp8_quant_group(float x0, float x1, bool v0, 
   const float expand = ratio <= 1.0f + QEPS ? 1.0f : fmaxf(raw_expand, 1.0f / EXPAND_MIN);
   const float smm = fmaxf(sqrtf(amax) * sqrtf(amin), QEPS);
   const float scale = fmaxf(powf(fmaxf(amax / smm, QEPS), expand) / FP8_MAX, QEPS);
-  auto enc = [&](float x, float a, bool valid) -> uint8_t {
-    const float np = powf(fmaxf(a / smm, QEPS), expand);
+  const float inv_smm = 1.0f / smm, inv_scale = 1.0f / scale;
+  float y[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float a = fabsf(x[k]);
+    const float np = pow_pos(fmaxf(a * inv_smm, QEPS), expand);
     float nrm = 0.f;
-    if (valid && a > 0.f) nrm = sgn ? (x >= 0.f ? np : -np) : np;
-    return e4m3_encode(nrm / scale);
-  };
-  q0 = enc(x0, a0, v0);
-  q1 = enc(x1, a1, v1);
+    if (k < nvalid && a > 0.f) nrm = sgn ? copysignf(np, x[k]) : np;
+    y[k] = __builtin_amdgcn_fmed3f(nrm * inv_scale, -FP8_MAX, FP8_MAX);
+  }
+  codes = e4m3_encode8(y);
   return Fp8Meta{scale, expand, smm};
 }
 
