@@ -140,11 +140,12 @@ def stage_flops(kind, gl):
 
 def stage_exec_flops(kind, gl):
     """MFMA FLOPs the kernels execute (padded tiles; symmetric stages compute the
-    upper-triangle tiles only)."""
+    256x256 tiles above the diagonal, and on a diagonal tile the 36 of its 64
+    32x32 MFMA tiles on or above the diagonal)."""
     lay = gl.ws.layout
     N, mp, np_ = gl.nblocks, lay.mp, lay.np_
     nt = mp // 256
-    sym = nt * (nt + 1) / 2 / (nt * nt)
+    sym = (nt * (nt - 1) / 2 + nt * 36 / 64) / (nt * nt)
     kx = -(-lay.n // 64) * 64
     if kind == "syrk":
         return 2.0 * mp * mp * kx * N * sym
@@ -158,6 +159,15 @@ def stage_exec_flops(kind, gl):
 def pack_bytes(gl, momentum_bytes, grad_bytes=2, x_bytes=2):
     lay = gl.ws.layout
     return gl.nblocks * lay.m * lay.n * (grad_bytes + 2 * momentum_bytes + x_bytes)
+
+
+def adamw_bytes(w):
+    """Algorithmic AdamW bytes: param read + write, grad read, both moments read
+    + write (1-byte codes on the FP8 path, metadata not counted)."""
+    from monarch_muon_amd.workloads import adamw_elements
+    pb = torch.empty((), dtype=w.param_dtype).element_size()
+    sb = 1 if w.momentum_dtype == "fp8" else pb
+    return adamw_elements(w) * (3 * pb + 4 * sb)
 
 
 def hbm_traffic(workload, kernel):
@@ -313,7 +323,9 @@ def main():
         "momentum_pack": {"ms": round(pack_ms, 3), "alg_bytes": pack_b,
                           "gbs": round(pack_b / (pack_ms * 1e-3) / 1e9, 1),
                           "frac_hbm": round(pack_b / (pack_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+        "muon_group_ms": round(sum(stage_ms[k] for k in ("pack", "syrk", "poly", "px")) / reps, 3),
         "adamw_ms": round(stage_ms["adamw"] / reps, 3),
+        "adamw_gbs": round(adamw_bytes(w) / (stage_ms["adamw"] / reps * 1e-3) / 1e9, 1),
         "kernels": kernels,
         "reference_h100_ms": REFERENCE_H100_MS,
     }
