@@ -108,7 +108,7 @@ def instrumented_step(opt, lr=0.02):
     return [(k, gl, it, e0.elapsed_time(e1)) for k, gl, it, e0, e1 in out]
 
 
-def kernel_symbol(kind, gl, it):
+def kernel_symbol(kind, gl, it, fp8=False):
     """The kernel (template instance) rocprof reports for a launch, as it
     appears in ``rocprofv3 --stats`` names (mmuon::(anonymous namespace)::...)."""
     if kind == "syrk":
@@ -121,8 +121,8 @@ def kernel_symbol(kind, gl, it):
         tp = "BF16T" if gl.struct.param_dtype == 1 else "F32T"
         return f"ns_px_bf16<3, {'true' if gl.transposed else 'false'}, {tp}>"
     if kind == "pack":
-        return "pack_cols_kernel" if gl.transposed else "pack_rows_kernel"
-    return kind + "_kernel"
+        return ("fp8_" if fp8 else "") + ("pack_cols_kernel" if gl.transposed else "pack_rows_kernel")
+    return kind + ("_fp8_kernel" if fp8 else "_kernel")
 
 
 def stage_flops(kind, gl):
@@ -277,7 +277,7 @@ def main():
     stage_ms = defaultdict(float)
     for _ in range(max(1, args.instrumented)):
         for kind, gl, it, ms in instrumented_step(opt):
-            sym = kernel_symbol(kind, gl, it)
+            sym = kernel_symbol(kind, gl, it, fp8=w.momentum_dtype == "fp8")
             rec = per[sym]
             rec[0] += ms
             rec[1] += 1
