@@ -90,6 +90,8 @@ typedef struct mmuon_group {
   void* p;                       /* workspace: polynomial (layout.a_bytes)       */
   float* partial;                /* workspace: layout.part_bytes                 */
   float* scale;                  /* workspace: N floats                          */
+  const float* grad_scale;       /* device: gradient-clipping coefficient from
+                                    mmuon_grad_clip_coef, or NULL (no clipping)  */
 } mmuon_group;
 
 /* Geometry and workspace sizes for a group of (rows x cols) blocks.
@@ -99,7 +101,9 @@ int mmuon_ns_layout(int32_t rows, int32_t cols, int32_t ns_dtype, int64_t nblock
                     mmuon_ns_layout_t* out);
 
 /* Heavy-ball momentum + stack + cast, in one pass over the group:
-     buf <- momentum*buf + grad          (rounded to the buffer dtype per op)
+     buf <- momentum*buf + grad          (rounded to the buffer dtype per op;
+                                          grad = dtype(grad * *grad_scale) when
+                                          g->grad_scale is set)
      X   <- cast(buf) to ns_dtype, transposed when rows > cols, into g->x0
      scale[b] <- 1 / (||X_b||_F + 1e-7), the Frobenius normalisation factor
    Replaces membench monarch_muon.py:146-151 (_foreach_mul_/_foreach_add_),
@@ -161,6 +165,7 @@ typedef struct mmuon_adamw_args {
   float sqrt_bc2;                    /* sqrt(1 - beta2 ** step)                        */
   float eps;
   float neg_step_size;               /* -lr / (1 - beta1 ** step)                      */
+  const float* grad_scale;           /* device clipping coefficient, or NULL           */
 } mmuon_adamw_args;
 
 /* Replaces membench monarch_muon.py:176-208 (foreach AdamW: decoupled weight
@@ -188,6 +193,42 @@ int mmuon_fp8_quantize(const float* value, uint8_t* codes, float* scale, float* 
 int mmuon_fp8_dequantize(const uint8_t* codes, const float* scale, const float* expand,
                          const float* sqrt_minmax, float* out, int64_t numel,
                          int32_t signed_, void* stream);
+
+/* Gradient-norm clipping folded into the step.  Computes, over the listed
+   gradients (one dtype, F32 or BF16), what torch.nn.utils.clip_grad_norm_
+   (norm_type 2) computes before it rescales them:
+     norm_t = dtype(sqrt(sum g^2))          per tensor, fp32 accumulation
+     total  = dtype(sqrt(sum norm_t^2))
+     coef   = min(dtype(dtype(1 / dtype(total + 1e-6)) * max_norm), 1)
+   (dtype(.) rounds to the gradients' dtype; torch evaluates `max_norm / t` as
+   t.reciprocal() * max_norm), writes total and coef, and leaves
+   the gradients untouched.  A group or AdamW launch whose grad_scale points at
+   coef then reads every gradient as dtype(g * coef), the value torch's in-place
+   rescale leaves in p.grad.  Chunks: tensor << 40 | first element, chunk_elems
+   elements each, every tensor's chunks contiguous and in tensor order;
+   first_chunk[t] = index of tensor t's first chunk, first_chunk[ntensors] =
+   nchunks.  partial: nchunks floats, norms: ntensors floats (workspace).
+   Replaces pretrain/src/optim/base.py:121-122 (clip_grad_norm_ before
+   opt.step(); its in-place rescale pass over the gradients is not needed). */
+typedef struct mmuon_grad_tensor {
+  const void* grad;
+  int64_t numel;
+} mmuon_grad_tensor;
+typedef struct mmuon_grad_norm_args {
+  const mmuon_grad_tensor* tensors;  /* device table, ntensors entries */
+  const int64_t* chunks;             /* device, nchunks entries        */
+  const int64_t* first_chunk;        /* device, ntensors + 1 entries   */
+  int64_t nchunks;
+  int32_t ntensors;
+  int32_t chunk_elems;
+  int32_t grad_dtype;
+  float max_norm;
+  float* partial;
+  float* norms;
+  float* total;                      /* device, 1 float (out) */
+  float* coef;                       /* device, 1 float (out) */
+} mmuon_grad_norm_args;
+int mmuon_grad_clip_coef(const mmuon_grad_norm_args* a, void* stream);
 
 /* Thread-local message of the last failing call ("" if none). */
 const char* mmuon_last_error(void);

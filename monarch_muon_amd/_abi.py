@@ -16,7 +16,7 @@ LIB_PATH = Path(os.environ.get("MMUON_LIB", Path(__file__).resolve().parent / "l
 F32, BF16, F8E4M3 = 0, 1, 2
 GROUP_ALIGNED16 = 1
 NS_NO_APPLY = 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8E4M3}
 
@@ -48,7 +48,7 @@ class Group(C.Structure):
                 ("ns_dtype", C.c_int32), ("flags", C.c_int32),
                 ("blocks", C.c_void_p), ("fp8", C.c_void_p),
                 ("x0", C.c_void_p), ("x1", C.c_void_p), ("a", C.c_void_p), ("p", C.c_void_p),
-                ("partial", C.c_void_p), ("scale", C.c_void_p)]
+                ("partial", C.c_void_p), ("scale", C.c_void_p), ("grad_scale", C.c_void_p)]
 
 
 class AdamWTensor(C.Structure):
@@ -62,12 +62,24 @@ class AdamWArgs(C.Structure):
                 ("state_dtype", C.c_int32), ("apply_weight_decay", C.c_int32),
                 ("wd_factor", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float),
                 ("one_minus_beta1", C.c_float), ("one_minus_beta2", C.c_float),
-                ("sqrt_bc2", C.c_float), ("eps", C.c_float), ("neg_step_size", C.c_float)]
+                ("sqrt_bc2", C.c_float), ("eps", C.c_float), ("neg_step_size", C.c_float),
+                ("grad_scale", C.c_void_p)]
 
 
 class AdamWFp8Tensor(C.Structure):
     _fields_ = [("scale_m", C.c_void_p), ("expand_m", C.c_void_p), ("sqrt_minmax_m", C.c_void_p),
                 ("scale_v", C.c_void_p), ("expand_v", C.c_void_p), ("sqrt_minmax_v", C.c_void_p)]
+
+
+class GradTensor(C.Structure):
+    _fields_ = [("grad", C.c_void_p), ("numel", C.c_int64)]
+
+
+class GradNormArgs(C.Structure):
+    _fields_ = [("tensors", C.c_void_p), ("chunks", C.c_void_p), ("first_chunk", C.c_void_p),
+                ("nchunks", C.c_int64), ("ntensors", C.c_int32), ("chunk_elems", C.c_int32),
+                ("grad_dtype", C.c_int32), ("max_norm", C.c_float), ("partial", C.c_void_p),
+                ("norms", C.c_void_p), ("total", C.c_void_p), ("coef", C.c_void_p)]
 
 
 # name -> (restype, argtypes)
@@ -88,6 +100,7 @@ SIGNATURES = {
                                      C.c_int64, C.c_int32, C.c_void_p]),
     "mmuon_fp8_dequantize": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                        C.c_int64, C.c_int32, C.c_void_p]),
+    "mmuon_grad_clip_coef": (C.c_int, [C.POINTER(GradNormArgs), C.c_void_p]),
 }
 
 _lib = None

@@ -97,6 +97,7 @@ mmuon::PackArgs pack_args(const mmuon_group* g, const Geometry& geo, float mu, i
   a.np = geo.np_;
   a.nparts = nparts;
   a.mu = mu;
+  a.gscale = g->grad_scale;
   return a;
 }
 
@@ -106,7 +107,7 @@ extern "C" {
 
 const char* mmuon_last_error(void) { return g_err.c_str(); }
 
-int mmuon_abi_version(void) { return 1; }
+int mmuon_abi_version(void) { return 2; }
 
 int mmuon_ns_layout(int32_t rows, int32_t cols, int32_t ns_dtype, int64_t nblocks,
                     mmuon_ns_layout_t* out) {
@@ -275,6 +276,7 @@ mmuon::AdamWArgs adamw_args(const mmuon_adamw_args* a) {
   k.sqrt_bc2 = a->sqrt_bc2;
   k.eps = a->eps;
   k.neg_step_size = a->neg_step_size;
+  k.gscale = a->grad_scale;
   return k;
 }
 }  // namespace
@@ -323,6 +325,20 @@ int mmuon_fp8_dequantize(const uint8_t* codes, const float* scale, const float* 
   mmuon::launch_fp8_dequantize(codes, scale, expand, sqrt_minmax, out, numel, signed_ != 0,
                                static_cast<hipStream_t>(stream));
   return check_launch("mmuon_fp8_dequantize");
+}
+
+int mmuon_grad_clip_coef(const mmuon_grad_norm_args* a, void* stream) {
+  if (a == nullptr) return fail(MMUON_EINVAL, "null gradient-norm arguments");
+  if (a->grad_dtype != MMUON_F32 && a->grad_dtype != MMUON_BF16)
+    return fail(MMUON_EINVAL, "gradient dtype must be F32 or BF16");
+  if (a->nchunks < 0 || a->ntensors < 0) return fail(MMUON_EINVAL, "negative chunk or tensor count");
+  if (a->nchunks > 0x7fffffff) return fail(MMUON_ERANGE, "too many gradient chunks");
+  if (a->chunk_elems <= 0) return fail(MMUON_EINVAL, "chunk_elems must be positive");
+  if (!a->total || !a->coef || !a->norms || (a->nchunks > 0 && (!a->tensors || !a->chunks || !a->partial)) ||
+      !a->first_chunk)
+    return fail(MMUON_EINVAL, "null gradient-norm pointer");
+  mmuon::launch_grad_clip_coef(*a, static_cast<hipStream_t>(stream));
+  return check_launch("mmuon_grad_clip_coef");
 }
 
 }  // extern "C"

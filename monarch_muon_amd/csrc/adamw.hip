@@ -66,7 +66,7 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_kernel(AdamWArgs a) {
         if (h == 1 && !two) break;
         const int64_t i = h ? i1 : i0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) adamw_elem<TP, TS>(P[h][e], G[h][e], M[h][e], V[h][e], a);
+        for (int e = 0; e < 8; ++e) adamw_elem<TP, TS>(P[h][e], clipped<TG>(G[h][e], a.gscale), M[h][e], V[h][e], a);
         Vec8<TP>::store(p + i, P[h]);
         Vec8<TS>::store(m + i, M[h]);
         Vec8<TS>::store(v + i, V[h]);
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_kernel(AdamWArgs a) {
   }
   for (int64_t i = tail + threadIdx.x; i < end; i += ADAM_NT) {
     float pv = TP::load(p, i), mv = TS::load(m, i), vv = TS::load(v, i);
-    adamw_elem<TP, TS>(pv, TG::load(g, i), mv, vv, a);
+    adamw_elem<TP, TS>(pv, clipped<TG>(TG::load(g, i), a.gscale), mv, vv, a);
     TP::store(p, i, pv);
     TS::store(m, i, mv);
     TS::store(v, i, vv);
@@ -168,7 +168,7 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
                  false, v);
   }
 #pragma unroll
-  for (int k = 0; k < 8; ++k) adamw_elem<TP, F32T>(pv[k], gv[k], m[k], v[k], a);
+  for (int k = 0; k < 8; ++k) adamw_elem<TP, F32T>(pv[k], clipped<TG>(gv[k], a.gscale), m[k], v[k], a);
   if (vec) {
     Vec8<TP>::store(p + e0, pv);
   } else {

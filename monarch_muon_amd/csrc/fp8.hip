@@ -76,8 +76,8 @@ constexpr int F8_GPW = F8_NT / 16;  // 128-groups per workgroup: one per 16-lane
 template <class TG>
 __device__ __forceinline__ void fp8_momentum8(const uint8_t* q, const float* scale, const float* expand,
                                               const float* smm, int64_t grp, int64_t e0,
-                                              const typename TG::storage* g, float mu, int have_state,
-                                              float nv[8]) {
+                                              const typename TG::storage* g, const float* gscale, float mu,
+                                              int have_state, float nv[8]) {
   float old[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (have_state) {
     const uint2 c = *reinterpret_cast<const uint2*>(q + e0);
@@ -88,7 +88,7 @@ __device__ __forceinline__ void fp8_momentum8(const uint8_t* q, const float* sca
 #pragma unroll
   for (int k = 0; k < 8; ++k) {
     const float t = old[k] * mu;
-    nv[k] = t + gv[k];
+    nv[k] = t + clipped<TG>(gv[k], gscale);
   }
 }
 
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(F8_NT) void fp8_pack_rows_kernel(PackArgs a, const 
   if (grp < gpb) {  // uniform over the 16-lane row
     const int64_t e0 = grp * 128 + (threadIdx.x & 15) * 8;
     float nv[8];
-    fp8_momentum8<TG>(q, md.scale, md.expand, md.sqrt_minmax, grp, e0, g, a.mu, have_state, nv);
+    fp8_momentum8<TG>(q, md.scale, md.expand, md.sqrt_minmax, grp, e0, g, a.gscale, a.mu, have_state, nv);
     float xv[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(F8_NT) void fp8_pack_cols_kernel(PackArgs a, const 
     if (r < rows) {  // uniform over the 16-lane row
       const int64_t e0 = int64_t(r) * cols + c0 + sub * 8;
       const int64_t grp = e0 >> 7;
-      fp8_momentum8<TG>(q, md.scale, md.expand, md.sqrt_minmax, grp, e0, g, a.mu, have_state, nv);
+      fp8_momentum8<TG>(q, md.scale, md.expand, md.sqrt_minmax, grp, e0, g, a.gscale, a.mu, have_state, nv);
       fp8_store_group(q, md, grp, e0, nv);
     }
     float4* t4 = reinterpret_cast<float4*>(&tile[rl][sub * 8]);

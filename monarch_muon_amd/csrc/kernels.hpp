@@ -18,6 +18,7 @@ struct PackArgs {
   int nparts;
   float mu;
   int vec;          // 8-wide vector access is valid for every block
+  const float* gscale;  // gradient-clipping coefficient (device), or null
 };
 
 int pack_nparts(int mp, int np_, bool transposed);
@@ -63,10 +64,20 @@ struct AdamWArgs {
   float neg_step_size;  // -lr / (1 - beta1^t)
   const mmuon_adamw_fp8_tensor* fp8;
   int have_state;
+  const float* gscale;  // gradient-clipping coefficient (device), or null
 };
 int launch_adamw(const AdamWArgs& a, int param_dtype, int grad_dtype, int state_dtype,
                  hipStream_t s);
 int launch_adamw_fp8(const AdamWArgs& a, int param_dtype, int grad_dtype, hipStream_t s);
+
+// Gradient-norm clipping coefficient --------------------------------------------
+int launch_grad_clip_coef(const mmuon_grad_norm_args& a, hipStream_t s);
+
+// Gradient as the step reads it: dtype(g * c) when clipping, else g.
+template <class TG>
+__device__ __forceinline__ float clipped(float g, const float* gscale) {
+  return gscale != nullptr ? TG::round(g * *gscale) : g;
+}
 
 // FP8 codec -------------------------------------------------------------------
 void launch_fp8_quantize(const float* v, uint8_t* q, float* sc, float* ex, float* smm,

@@ -60,7 +60,7 @@ __global__ __launch_bounds__(PACK_NT) void pack_rows_kernel(PackArgs a) {
         float v[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-          bv[it][q] = momentum_update<TB>(bv[it][q], gv[it][q], a.mu);
+          bv[it][q] = momentum_update<TB>(bv[it][q], clipped<TG>(gv[it][q], a.gscale), a.mu);
           v[q] = TX::round(bv[it][q]);
           ss += v[q] * v[q];
         }
@@ -91,7 +91,7 @@ __global__ __launch_bounds__(PACK_NT) void pack_rows_kernel(PackArgs a) {
       Vec8<TG>::load(g + s, gv);
       Vec8<TB>::load(buf + s, bv);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) bv[q] = momentum_update<TB>(bv[q], gv[q], a.mu);
+      for (int q = 0; q < 8; ++q) bv[q] = momentum_update<TB>(bv[q], clipped<TG>(gv[q], a.gscale), a.mu);
       Vec8<TB>::store(buf + s, bv);
 #pragma unroll
       for (int q = 0; q < 8; ++q) v[q] = TX::round(bv[q]);
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(PACK_NT) void pack_rows_kernel(PackArgs a) {
         v[q] = 0.f;
         if (i < a.m && j + q < a.n) {
           const int64_t s = int64_t(i) * a.n + j + q;
-          const float nb = momentum_update<TB>(TB::load(buf, s), TG::load(g, s), a.mu);
+          const float nb = momentum_update<TB>(TB::load(buf, s), clipped<TG>(TG::load(g, s), a.gscale), a.mu);
           TB::store(buf, s, nb);
           v[q] = TX::round(nb);
         }
@@ -155,7 +155,7 @@ __global__ __launch_bounds__(PACK_NT) void pack_cols_kernel(PackArgs a) {
       float v[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        bv[q][k] = momentum_update<TB>(bv[q][k], gv[q][k], a.mu);
+        bv[q][k] = momentum_update<TB>(bv[q][k], clipped<TG>(gv[q][k], a.gscale), a.mu);
         v[k] = TX::round(bv[q][k]);
         ss += v[k] * v[k];
       }
@@ -174,7 +174,7 @@ __global__ __launch_bounds__(PACK_NT) void pack_cols_kernel(PackArgs a) {
         float v = 0.f;
         if (r < a.n && c + k < a.m) {
           const int64_t s = int64_t(r) * a.m + c + k;
-          const float nb = momentum_update<TB>(TB::load(buf, s), TG::load(g, s), a.mu);
+          const float nb = momentum_update<TB>(TB::load(buf, s), clipped<TG>(TG::load(g, s), a.gscale), a.mu);
           TB::store(buf, s, nb);
           v = TX::round(nb);
         }

@@ -18,7 +18,7 @@ import ctypes as C
 import torch
 
 from . import _abi
-from .plan import NS_COEFFS, NS_STEPS, AdamPlanner, MuonPlanner, adamw_scalars
+from .plan import NORM_CHUNK, NS_COEFFS, NS_STEPS, AdamPlanner, MuonPlanner, NormPlanner, adamw_scalars
 
 _COEFFS = (C.c_float * 3)(*NS_COEFFS)
 
@@ -53,6 +53,8 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
         self.ns_dtype = ns_dtype
         self._muon_planner = MuonPlanner()
         self._adam_planner = AdamPlanner()
+        self._norm_planner = NormPlanner()
+        self._clip = None    # device clipping coefficient for the next step (clip_grad_norm_)
         self._timing = None  # optional per-launch hipEvent capture, used by bench.py
 
     # ------------------------------------------------------------------
@@ -62,18 +64,73 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
-        for group in self.param_groups:
-            lr = group["lr"]
-            if group["update_type"] == "muon":
-                self._muon_step(group, lr)
-            else:
-                self._adamw_step(group, lr)
+        try:
+            for group in self.param_groups:
+                lr = group["lr"]
+                if group["update_type"] == "muon":
+                    self._muon_step(group, lr)
+                else:
+                    self._adamw_step(group, lr)
+        finally:
+            self._clip = None  # a clipping coefficient applies to one step
         return loss
+
+    def _grad_scale(self):
+        return self._clip.data_ptr() if self._clip is not None else None
+
+    @torch.no_grad()
+    def clip_grad_norm_(self, max_norm: float, norm_type: float = 2.0,
+                        error_if_nonfinite: bool = False) -> torch.Tensor:
+        """``torch.nn.utils.clip_grad_norm_`` over this optimizer's parameters,
+        folded into the next ``step()``.
+
+        The reference clips right before the step
+        (``pretrain/src/optim/base.py:121-122``:
+        ``torch.nn.utils.clip_grad_norm_(model.parameters(), grad_clip)``, then
+        ``opt.step()``).  Here the per-tensor norms, their norm and the
+        coefficient ``min(max_norm / (total + 1e-6), 1)`` are computed on the
+        device, rounded to the gradients' dtype where torch rounds them, and the
+        next ``step()`` reads every gradient as ``dtype(g * coef)`` -- the value
+        torch's in-place rescale leaves in ``p.grad``.  The gradients are not
+        rewritten, so the rescale pass over them is saved, and nothing
+        synchronises with the host.  Returns the total norm (0-dim tensor in the
+        gradients' dtype, on the device).  The 2-norm only; every gradient on one
+        device, in one dtype.
+        """
+        if float(norm_type) != 2.0:
+            raise NotImplementedError("the fused clip_grad_norm_ computes the 2-norm only")
+        grads = [p.grad for group in self.param_groups for p in group["params"] if p.grad is not None]
+        if not grads:
+            self._clip = None
+            return torch.tensor(0.0)
+        for g in grads:
+            _require_gpu(g)
+        grads = [g if g.is_contiguous() else g.contiguous() for g in grads]
+        nl = self._norm_planner.plan(grads)
+        args = _abi.GradNormArgs(tensors=nl.tensors.data_ptr(), chunks=nl.chunks.data_ptr(),
+                                 first_chunk=nl.first_chunk.data_ptr(), nchunks=nl.nchunks, ntensors=nl.ntensors,
+                                 chunk_elems=NORM_CHUNK, grad_dtype=_abi.dtype_code(nl.dtype),
+                                 max_norm=float(max_norm), partial=nl.partial.data_ptr(), norms=nl.norms.data_ptr(),
+                                 total=nl.total.data_ptr(), coef=nl.coef.data_ptr())
+        _abi.check(_abi.lib().mmuon_grad_clip_coef(C.byref(args), _abi.stream_handle(grads[0].device)),
+                   "mmuon_grad_clip_coef")
+        total = nl.total.to(nl.dtype, copy=True).reshape(())  # the value is exact in the gradients' dtype
+        if error_if_nonfinite and not bool(torch.isfinite(total)):
+            raise RuntimeError(f"The total norm of order {float(norm_type)} for gradients from `parameters` is "
+                               "non-finite, so it cannot be clipped. To disable this error and scale the gradients "
+                               "by the non-finite norm anyway, set `error_if_nonfinite=False`")
+        self._clip = nl.coef
+        return total
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        self._clip = None  # the coefficient belongs to the gradients being dropped
+        super().zero_grad(set_to_none=set_to_none)
 
     def release_workspace(self) -> None:
         """Drop the cached Newton-Schulz workspaces and launch tables."""
         self._muon_planner.release()
         self._adam_planner.release()
+        self._norm_planner.release()
 
     # ------------------------------------------------------------------
     # Muon (membench :134-170, pretrain :133-165)
@@ -101,6 +158,7 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
         lib = _abi.lib()
         for gl in launches:
             stream = _abi.stream_handle(gl.key[0])
+            gl.struct.grad_scale = self._grad_scale()
             ev = self._mark("pack")
             _abi.check(lib.mmuon_momentum_pack(C.byref(gl.struct), momentum, stream), "mmuon_momentum_pack")
             self._mark_end(ev)
@@ -155,7 +213,7 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
         args = _abi.AdamWArgs(tensors=al.tensors.data_ptr(), chunks=al.chunks.data_ptr(), nchunks=al.nchunks,
                               chunk_elems=al.chunk, param_dtype=_abi.dtype_code(al.pd),
                               grad_dtype=_abi.dtype_code(al.gd), state_dtype=_abi.dtype_code(al.sd),
-                              **adamw_scalars(lr, beta1, beta2, eps, wd, step))
+                              grad_scale=self._grad_scale(), **adamw_scalars(lr, beta1, beta2, eps, wd, step))
         stream = _abi.stream_handle(al.tensors.device)
         ev = self._mark("adamw")
         if al.fp8 is not None:
@@ -277,6 +335,7 @@ class CoatStateMonarchMuon(MonarchMuonOptimizer):
         lib = _abi.lib()
         for gl in launches:
             stream = _abi.stream_handle(gl.key[0])
+            gl.struct.grad_scale = self._grad_scale()
             ev = self._mark("pack")
             _abi.check(lib.mmuon_fp8_momentum_pack(C.byref(gl.struct), momentum, 1, stream),
                        "mmuon_fp8_momentum_pack")

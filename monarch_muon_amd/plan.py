@@ -249,3 +249,61 @@ def adamw_scalars(lr, beta1, beta2, eps, weight_decay, step) -> dict:
     return dict(apply_weight_decay=int(weight_decay > 0), wd_factor=1.0 - lr * weight_decay,
                 beta1=beta1, beta2=beta2, one_minus_beta1=1.0 - beta1, one_minus_beta2=1.0 - beta2,
                 sqrt_bc2=math.sqrt(bc2), eps=eps, neg_step_size=-lr / bc1)
+
+
+# ---------------------------------------------------------------------------
+# Gradient-norm clipping (the norm pass of torch.nn.utils.clip_grad_norm_)
+# ---------------------------------------------------------------------------
+NORM_CHUNK = 8192
+
+
+@dataclass
+class NormLaunch:
+    dtype: torch.dtype
+    tensors: torch.Tensor         # device int64 [T, 2]: gradient pointer, numel
+    chunks: torch.Tensor          # device int64 [nchunks]: tensor << 40 | first element
+    first_chunk: torch.Tensor     # device int64 [T + 1]
+    nchunks: int
+    ntensors: int
+    partial: torch.Tensor         # fp32 [nchunks] workspace
+    norms: torch.Tensor           # fp32 [T] workspace
+    total: torch.Tensor           # fp32 [1]
+    coef: torch.Tensor            # fp32 [1]
+
+
+class NormPlanner:
+    """Device tables for the gradient-norm pass; rebuilt only when a gradient
+    pointer, dtype or size changes."""
+
+    def __init__(self):
+        self._sig = None
+        self._launch: NormLaunch | None = None
+
+    def release(self) -> None:
+        self._sig = None
+        self._launch = None
+
+    def plan(self, grads) -> NormLaunch:
+        sig = tuple((g.data_ptr(), g.dtype, g.numel(), g.device) for g in grads)
+        if sig == self._sig:
+            return self._launch
+        if len({g.dtype for g in grads}) != 1 or len({g.device for g in grads}) != 1:
+            raise NotImplementedError("fused gradient clipping needs every gradient on one device in one dtype")
+        for g in grads:
+            if not g.is_contiguous():
+                raise ValueError("gradients must be contiguous")
+        device = grads[0].device
+        tens, chunks, first = [], [], []
+        for t, g in enumerate(grads):
+            first.append(len(chunks))
+            n = g.numel()
+            tens.append((g.data_ptr(), n))
+            chunks.extend((t << 40) | s for s in range(0, n, NORM_CHUNK))
+        first.append(len(chunks))
+        f32 = dict(dtype=torch.float32, device=device)
+        self._launch = NormLaunch(grads[0].dtype, _h2d_int64(tens, device), _h2d_int64(chunks or [0], device),
+                                  _h2d_int64(first, device), len(chunks), len(grads),
+                                  torch.empty(max(1, len(chunks)), **f32), torch.empty(max(1, len(grads)), **f32),
+                                  torch.empty(1, **f32), torch.empty(1, **f32))
+        self._sig = sig
+        return self._launch
