@@ -235,6 +235,9 @@ def main():
     ap.add_argument("--workload", default="6.89b-nb4")
     ap.add_argument("--instrumented", type=int, default=2, help="extra per-kernel-timed steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--grad-clip", type=float, default=0.0,
+                    help="also clip the gradient norm before every timed step (opt.clip_grad_norm_), and report "
+                         "the fused clip and torch.nn.utils.clip_grad_norm_ on the same gradients")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (for HBM counter calibration)")
     args = ap.parse_args()
@@ -256,6 +259,8 @@ def main():
     muon, adamw, opt = build_gpu(w, dev)
     log(f"[bench] warm-up {args.warmup} steps")
     for _ in range(args.warmup):
+        if args.grad_clip:
+            opt.clip_grad_norm_(args.grad_clip)
         opt.step()
     torch.cuda.synchronize()
     log(f"[bench] timing {args.steps} steps")
@@ -264,6 +269,8 @@ def main():
     t0 = time.perf_counter()
     for s, e in evs:
         s.record()
+        if args.grad_clip:
+            opt.clip_grad_norm_(args.grad_clip)
         opt.step()
         e.record()
     torch.cuda.synchronize()
@@ -329,6 +336,25 @@ def main():
         "kernels": kernels,
         "reference_h100_ms": REFERENCE_H100_MS,
     }
+    if args.grad_clip:
+        params = muon + adamw
+
+        def timed(fn, reps=5):
+            fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(reps):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / reps
+
+        fused = timed(lambda: opt.clip_grad_norm_(args.grad_clip))
+        ref = timed(lambda: torch.nn.utils.clip_grad_norm_(params, args.grad_clip))  # rescales the grads in place
+        res["grad_clip"] = {"max_norm": args.grad_clip, "fused_clip_ms": round(fused, 3),
+                            "torch_clip_grad_norm_ms": round(ref, 3),
+                            "note": "value/ms_per_step include opt.clip_grad_norm_ before every step"}
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle on host cores, bounded sample)")
         res["cpu_baseline"] = cpu_baseline(w)
