@@ -101,47 +101,49 @@ int launch_adamw(const AdamWArgs& a, int param_dtype, int grad_dtype, int state_
 }
 
 // ---------------------------------------------------------------------------
-// FP8-state AdamW: one 128-element metadata group per 16-lane row, 8
-// consecutive elements per lane; the moments are dequantized to fp32, updated
-// in fp32 (the reference's dequantized states are fp32 tensors), and
+// FP8-state AdamW: one 128-element metadata group per F8_LANES lanes,
+// F8_ELEMS consecutive elements per lane; the moments are dequantized to fp32,
+// updated in fp32 (the reference's dequantized states are fp32 tensors), and
 // requantized (exp_avg signed, exp_avg_sq unsigned).
 // chunk = tensor << 40 | first element of the group.
 // ---------------------------------------------------------------------------
-constexpr int F8_GPW = ADAM_NT / 16;  // groups per workgroup
+constexpr int F8_GPW = ADAM_NT / F8_LANES;  // groups per workgroup
 
 template <class T>
-__device__ __forceinline__ void load8_masked(const typename T::storage* p, int64_t e0, int nvalid, bool vec,
-                                             float v[8]) {
+__device__ __forceinline__ void load_lane(const typename T::storage* p, int64_t e0, int nvalid, bool vec,
+                                          float v[F8_ELEMS]) {
   if (vec) {
     Vec8<T>::load(p + e0, v);
+    Vec8<T>::load(p + e0 + 8, v + 8);
     return;
   }
 #pragma unroll
-  for (int k = 0; k < 8; ++k) v[k] = k < nvalid ? T::load(p, e0 + k) : 0.f;
+  for (int k = 0; k < F8_ELEMS; ++k) v[k] = k < nvalid ? T::load(p, e0 + k) : 0.f;
 }
-__device__ __forceinline__ uint2 load_codes(const uint8_t* q, int64_t e0, int nvalid, bool vec) {
-  if (vec) return *reinterpret_cast<const uint2*>(q + e0);
-  uint32_t w[2] = {0u, 0u};
+__device__ __forceinline__ uint4 load_codes(const uint8_t* q, int64_t e0, int nvalid, bool vec) {
+  if (vec) return *reinterpret_cast<const uint4*>(q + e0);
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int k = 0; k < 8; ++k)
+  for (int k = 0; k < F8_ELEMS; ++k)
     if (k < nvalid) w[k >> 2] |= uint32_t(q[e0 + k]) << (8 * (k & 3));
-  return make_uint2(w[0], w[1]);
+  return make_uint4(w[0], w[1], w[2], w[3]);
 }
-__device__ __forceinline__ void store_codes(uint8_t* q, int64_t e0, int nvalid, bool vec, uint2 c) {
+__device__ __forceinline__ void store_codes(uint8_t* q, int64_t e0, int nvalid, bool vec, uint4 c) {
   if (vec) {
-    *reinterpret_cast<uint2*>(q + e0) = c;
+    *reinterpret_cast<uint4*>(q + e0) = c;
     return;
   }
+  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
-  for (int k = 0; k < 8; ++k)
-    if (k < nvalid) q[e0 + k] = uint8_t((k < 4 ? c.x : c.y) >> (8 * (k & 3)));
+  for (int k = 0; k < F8_ELEMS; ++k)
+    if (k < nvalid) q[e0 + k] = uint8_t(w[k >> 2] >> (8 * (k & 3)));
 }
 
 template <class TP, class TG>
 __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
-  const int64_t gidx = int64_t(blockIdx.x) * F8_GPW + (threadIdx.x >> 4);
-  if (gidx >= a.nchunks) return;  // whole 16-lane rows leave together
-  const int sub = threadIdx.x & 15;
+  const int64_t gidx = int64_t(blockIdx.x) * F8_GPW + (threadIdx.x / F8_LANES);
+  if (gidx >= a.nchunks) return;  // a group's lanes leave together
+  const int sub = threadIdx.x % F8_LANES;
   const int64_t code = a.chunks[gidx];
   const int t = int(code >> 40);
   const int64_t start = code & ((int64_t(1) << 40) - 1);
@@ -152,34 +154,37 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
   const auto* g = reinterpret_cast<const typename TG::storage*>(T.grad);
   uint8_t* qm = reinterpret_cast<uint8_t*>(T.exp_avg);
   uint8_t* qv = reinterpret_cast<uint8_t*>(T.exp_avg_sq);
-  const int64_t e0 = start + sub * 8;
-  const int nvalid = int(max(int64_t(0), min(int64_t(8), T.numel - e0)));
-  // 16-B parameter / gradient and 8-B code accesses for a full, aligned lane
-  const uintptr_t al = reinterpret_cast<uintptr_t>(p + e0) | reinterpret_cast<uintptr_t>(g + e0);
-  const bool vec = nvalid == 8 && (al & 15) == 0 &&
-                   ((reinterpret_cast<uintptr_t>(qm + e0) | reinterpret_cast<uintptr_t>(qv + e0)) & 7) == 0;
-  float pv[8], gv[8], m[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  load8_masked<TP>(p, e0, nvalid, vec, pv);
-  load8_masked<TG>(g, e0, nvalid, vec, gv);
+  const int64_t e0 = start + sub * F8_ELEMS;
+  const int nvalid = int(max(int64_t(0), min(int64_t(F8_ELEMS), T.numel - e0)));
+  // 16-B parameter / gradient / code accesses for a full, aligned lane
+  const uintptr_t al = reinterpret_cast<uintptr_t>(p + e0) | reinterpret_cast<uintptr_t>(g + e0) |
+                       reinterpret_cast<uintptr_t>(qm + e0) | reinterpret_cast<uintptr_t>(qv + e0);
+  const bool vec = nvalid == F8_ELEMS && (al & 15) == 0;
+  float pv[F8_ELEMS], gv[F8_ELEMS], m[F8_ELEMS], v[F8_ELEMS];
+#pragma unroll
+  for (int k = 0; k < F8_ELEMS; ++k) m[k] = v[k] = 0.f;
+  load_lane<TP>(p, e0, nvalid, vec, pv);
+  load_lane<TG>(g, e0, nvalid, vec, gv);
   if (a.have_state) {
-    fp8_dequant8(load_codes(qm, e0, nvalid, vec), fp8_dq(Fp8Meta{M.scale_m[grp], M.expand_m[grp], M.sqrt_minmax_m[grp]}),
-                 true, m);
-    fp8_dequant8(load_codes(qv, e0, nvalid, vec), fp8_dq(Fp8Meta{M.scale_v[grp], M.expand_v[grp], M.sqrt_minmax_v[grp]}),
-                 false, v);
+    fp8_dequant16(load_codes(qm, e0, nvalid, vec),
+                  fp8_dq(Fp8Meta{M.scale_m[grp], M.expand_m[grp], M.sqrt_minmax_m[grp]}), true, m);
+    fp8_dequant16(load_codes(qv, e0, nvalid, vec),
+                  fp8_dq(Fp8Meta{M.scale_v[grp], M.expand_v[grp], M.sqrt_minmax_v[grp]}), false, v);
   }
 #pragma unroll
-  for (int k = 0; k < 8; ++k) adamw_elem<TP, F32T>(pv[k], clipped<TG>(gv[k], a.gscale), m[k], v[k], a);
+  for (int k = 0; k < F8_ELEMS; ++k) adamw_elem<TP, F32T>(pv[k], clipped<TG>(gv[k], a.gscale), m[k], v[k], a);
   if (vec) {
     Vec8<TP>::store(p + e0, pv);
+    Vec8<TP>::store(p + e0 + 8, pv + 8);
   } else {
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
+    for (int k = 0; k < F8_ELEMS; ++k)
       if (k < nvalid) TP::store(p, e0 + k, pv[k]);
   }
-  uint2 c;
-  const Fp8Meta nm = fp8_quant16(m, nvalid, true, c);
+  uint4 c;
+  const Fp8Meta nm = fp8_quant_group(m, nvalid, true, c);
   store_codes(qm, e0, nvalid, vec, c);
-  const Fp8Meta nv = fp8_quant16(v, nvalid, false, c);
+  const Fp8Meta nv = fp8_quant_group(v, nvalid, false, c);
   store_codes(qv, e0, nvalid, vec, c);
   if (sub == 0) {
     M.scale_m[grp] = nm.scale;
