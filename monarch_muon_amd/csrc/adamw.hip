@@ -102,11 +102,12 @@ int launch_adamw(const AdamWArgs& a, int param_dtype, int grad_dtype, int state_
 
 // ---------------------------------------------------------------------------
 // FP8-state AdamW: one 128-element metadata group per F8_LANES lanes,
-// F8_ELEMS consecutive elements per lane; the moments are dequantized to fp32,
+// F8_ELEMS (16) consecutive elements per lane; the moments are dequantized to fp32,
 // updated in fp32 (the reference's dequantized states are fp32 tensors), and
 // requantized (exp_avg signed, exp_avg_sq unsigned).
 // chunk = tensor << 40 | first element of the group.
 // ---------------------------------------------------------------------------
+constexpr int F8_ELEMS = 16, F8_LANES = 128 / F8_ELEMS;
 constexpr int F8_GPW = ADAM_NT / F8_LANES;  // groups per workgroup
 
 template <class T>
@@ -166,10 +167,9 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
   load_lane<TP>(p, e0, nvalid, vec, pv);
   load_lane<TG>(g, e0, nvalid, vec, gv);
   if (a.have_state) {
-    fp8_dequant16(load_codes(qm, e0, nvalid, vec),
-                  fp8_dq(Fp8Meta{M.scale_m[grp], M.expand_m[grp], M.sqrt_minmax_m[grp]}), true, m);
-    fp8_dequant16(load_codes(qv, e0, nvalid, vec),
-                  fp8_dq(Fp8Meta{M.scale_v[grp], M.expand_v[grp], M.sqrt_minmax_v[grp]}), false, v);
+    const uint4 cm[1] = {load_codes(qm, e0, nvalid, vec)}, cv[1] = {load_codes(qv, e0, nvalid, vec)};
+    fp8_dequant_lane<F8_ELEMS>(cm, fp8_dq(Fp8Meta{M.scale_m[grp], M.expand_m[grp], M.sqrt_minmax_m[grp]}), true, m);
+    fp8_dequant_lane<F8_ELEMS>(cv, fp8_dq(Fp8Meta{M.scale_v[grp], M.expand_v[grp], M.sqrt_minmax_v[grp]}), false, v);
   }
 #pragma unroll
   for (int k = 0; k < F8_ELEMS; ++k) adamw_elem<TP, F32T>(pv[k], clipped<TG>(gv[k], a.gscale), m[k], v[k], a);
@@ -181,11 +181,11 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
     for (int k = 0; k < F8_ELEMS; ++k)
       if (k < nvalid) TP::store(p, e0 + k, pv[k]);
   }
-  uint4 c;
-  const Fp8Meta nm = fp8_quant_group(m, nvalid, true, c);
-  store_codes(qm, e0, nvalid, vec, c);
-  const Fp8Meta nv = fp8_quant_group(v, nvalid, false, c);
-  store_codes(qv, e0, nvalid, vec, c);
+  uint4 c[1];
+  const Fp8Meta nm = fp8_quant_group<F8_ELEMS>(m, nvalid, true, c);
+  store_codes(qm, e0, nvalid, vec, c[0]);
+  const Fp8Meta nv = fp8_quant_group<F8_ELEMS>(v, nvalid, false, c);
+  store_codes(qv, e0, nvalid, vec, c[0]);
   if (sub == 0) {
     M.scale_m[grp] = nm.scale;
     M.expand_m[grp] = nm.expand;

@@ -9,25 +9,26 @@ namespace mmuon {
 constexpr int F8_NT = 256;  // 4 waves = 4 groups per workgroup
 
 // coat_state_muon.py:103-114: fp32 values -> codes + per-group metadata.  One
-// group of 128 per F8_LANES lanes, F8_ELEMS consecutive elements per lane.
-constexpr int F8_GPW = F8_NT / F8_LANES;  // 128-groups per workgroup
+// group of 128 per QL lanes, QE consecutive elements per lane.
+constexpr int QE = 16, QL = 128 / QE;
+constexpr int Q_GPW = F8_NT / QL;  // 128-groups per workgroup
 
 __global__ __launch_bounds__(F8_NT) void fp8_quantize_kernel(const float* v, uint8_t* q, float* sc,
                                                              float* ex, float* smm, int64_t numel,
                                                              int sgn) {
-  const int64_t grp = int64_t(blockIdx.x) * F8_GPW + (threadIdx.x / F8_LANES);
+  const int64_t grp = int64_t(blockIdx.x) * Q_GPW + (threadIdx.x / QL);
   if (grp * 128 >= numel) return;  // a group's lanes leave together
-  const int sub = threadIdx.x % F8_LANES;
-  const int64_t e0 = grp * 128 + sub * F8_ELEMS;
-  const int nvalid = int(max(int64_t(0), min(int64_t(F8_ELEMS), numel - e0)));
-  float x[F8_ELEMS];
+  const int sub = threadIdx.x % QL;
+  const int64_t e0 = grp * 128 + sub * QE;
+  const int nvalid = int(max(int64_t(0), min(int64_t(QE), numel - e0)));
+  float x[QE];
 #pragma unroll
-  for (int k = 0; k < F8_ELEMS; ++k) x[k] = k < nvalid ? v[e0 + k] : 0.f;
-  uint4 c;
-  const Fp8Meta md = fp8_quant_group(x, nvalid, sgn != 0, c);
-  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+  for (int k = 0; k < QE; ++k) x[k] = k < nvalid ? v[e0 + k] : 0.f;
+  uint4 c[QE / 16];
+  const Fp8Meta md = fp8_quant_group<QE>(x, nvalid, sgn != 0, c);
+  const uint32_t w[4] = {c[0].x, c[0].y, c[0].z, c[0].w};
 #pragma unroll
-  for (int k = 0; k < F8_ELEMS; ++k)
+  for (int k = 0; k < QE; ++k)
     if (k < nvalid) q[e0 + k] = uint8_t(w[k >> 2] >> (8 * (k & 3)));
   if (sub == 0) {
     sc[grp] = md.scale;
@@ -50,7 +51,7 @@ void launch_fp8_quantize(const float* v, uint8_t* q, float* sc, float* ex, float
                          int64_t numel, bool sgn, hipStream_t s) {
   const int64_t groups = (numel + 127) / 128;
   if (groups == 0) return;
-  hipLaunchKernelGGL(fp8_quantize_kernel, dim3(unsigned((groups + F8_GPW - 1) / F8_GPW)), dim3(F8_NT), 0, s, v, q,
+  hipLaunchKernelGGL(fp8_quantize_kernel, dim3(unsigned((groups + Q_GPW - 1) / Q_GPW)), dim3(F8_NT), 0, s, v, q,
                      sc, ex, smm, numel, int(sgn));
 }
 
@@ -68,54 +69,61 @@ void launch_fp8_dequantize(const uint8_t* q, const float* sc, const float* ex, c
 // (coat_state_muon.py:126-139).  The momentum is not touched between its update
 // and the requantization, so both happen here in one pass.
 // ---------------------------------------------------------------------------
-// This lane's F8_ELEMS momentum values after the update: dequantized codes
-// (zeros without state) * mu + g, each op rounded to fp32 as the reference's
-// fp32 foreach ops round.
+// The fused pack: one 128-group per PL lanes, PE consecutive elements per lane.
+constexpr int PE = 32, PL = 128 / PE;
+constexpr int P_GPW = F8_NT / PL;  // 128-groups per workgroup
+
+// This lane's PE momentum values after the update: dequantized codes (zeros
+// without state) * mu + g, each op rounded to fp32 as the reference's fp32
+// foreach ops round.
 template <class TG>
 __device__ __forceinline__ void fp8_momentum_lane(const uint8_t* q, const float* scale, const float* expand,
                                                   const float* smm, int64_t grp, int64_t e0,
                                                   const typename TG::storage* g, const float* gscale, float mu,
-                                                  int have_state, float nv[F8_ELEMS]) {
-  float old[F8_ELEMS];
+                                                  int have_state, float (&nv)[PE]) {
+  float old[PE];
 #pragma unroll
-  for (int k = 0; k < F8_ELEMS; ++k) old[k] = 0.f;
+  for (int k = 0; k < PE; ++k) old[k] = 0.f;
   if (have_state) {
-    const uint4 c = *reinterpret_cast<const uint4*>(q + e0);
-    fp8_dequant16(c, fp8_dq(Fp8Meta{scale[grp], expand[grp], smm[grp]}), true, old);
-  }
-  float gv[F8_ELEMS];
-  Vec8<TG>::load(g + e0, gv);
-  Vec8<TG>::load(g + e0 + 8, gv + 8);
+    uint4 c[PE / 16];
 #pragma unroll
-  for (int k = 0; k < F8_ELEMS; ++k) {
+    for (int h = 0; h < PE / 16; ++h) c[h] = *reinterpret_cast<const uint4*>(q + e0 + 16 * h);
+    fp8_dequant_lane<PE>(c, fp8_dq(Fp8Meta{scale[grp], expand[grp], smm[grp]}), true, old);
+  }
+  float gv[PE];
+#pragma unroll
+  for (int h = 0; h < PE / 8; ++h) Vec8<TG>::load(g + e0 + 8 * h, gv + 8 * h);
+#pragma unroll
+  for (int k = 0; k < PE; ++k) {
     const float t = old[k] * mu;
     nv[k] = t + clipped<TG>(gv[k], gscale);
   }
 }
 
 __device__ __forceinline__ void fp8_store_group(uint8_t* q, const mmuon_block_fp8& md, int64_t grp, int64_t e0,
-                                                const float nv[F8_ELEMS]) {
-  uint4 c;
-  const Fp8Meta nm = fp8_quant_group(nv, F8_ELEMS, true, c);
-  *reinterpret_cast<uint4*>(q + e0) = c;
-  if (threadIdx.x % F8_LANES == 0) {
+                                                const float (&nv)[PE]) {
+  uint4 c[PE / 16];
+  const Fp8Meta nm = fp8_quant_group<PE>(nv, PE, true, c);
+#pragma unroll
+  for (int h = 0; h < PE / 16; ++h) *reinterpret_cast<uint4*>(q + e0 + 16 * h) = c[h];
+  if (threadIdx.x % PL == 0) {
     md.scale[grp] = nm.scale;
     md.expand[grp] = nm.expand;
     md.sqrt_minmax[grp] = nm.sqrt_minmax;
   }
 }
 
-// A group of F8_LANES lanes per 128-group of a block (groups may wrap rows),
-// F8_ELEMS elements per lane.  TRANS: the block is tall (rows > cols) and X
-// holds its transpose; the fallback for tall blocks whose width is not a
-// multiple of 128 (scattered X stores).
+// PL lanes per 128-group of a block (groups may wrap rows), PE elements per
+// lane.  TRANS: the block is tall (rows > cols) and X holds its transpose; the
+// fallback for tall blocks whose width is not a multiple of 128 (scattered X
+// stores).
 template <class TG, class TX, bool TRANS>
 __global__ __launch_bounds__(F8_NT) void fp8_pack_rows_kernel(PackArgs a, const mmuon_block_fp8* meta,
                                                               int rows, int cols, int have_state) {
   __shared__ float red[F8_NT / 64];
   const int b = blockIdx.y;
   const int64_t gpb = int64_t(rows) * cols / 128;  // groups per block
-  const int64_t grp = int64_t(blockIdx.x) * F8_GPW + (threadIdx.x / F8_LANES);
+  const int64_t grp = int64_t(blockIdx.x) * P_GPW + (threadIdx.x / PL);
   const mmuon_block_ref ref = a.blocks[b];
   const mmuon_block_fp8 md = meta[b];
   const auto* g = reinterpret_cast<const typename TG::storage*>(ref.grad);
@@ -123,23 +131,23 @@ __global__ __launch_bounds__(F8_NT) void fp8_pack_rows_kernel(PackArgs a, const 
   auto* x = reinterpret_cast<typename TX::storage*>(a.x) + int64_t(b) * a.mp * a.np;
   float ss = 0.f;
   if (grp < gpb) {  // uniform over the group's lanes
-    const int64_t e0 = grp * 128 + (threadIdx.x % F8_LANES) * F8_ELEMS;
-    float nv[F8_ELEMS];
+    const int64_t e0 = grp * 128 + (threadIdx.x % PL) * PE;
+    float nv[PE];
     fp8_momentum_lane<TG>(q, md.scale, md.expand, md.sqrt_minmax, grp, e0, g, a.gscale, a.mu, have_state, nv);
-    float xv[F8_ELEMS];
+    float xv[PE];
 #pragma unroll
-    for (int k = 0; k < F8_ELEMS; ++k) {
+    for (int k = 0; k < PE; ++k) {
       xv[k] = TX::round(nv[k]);
       ss += xv[k] * xv[k];
     }
-    if (!TRANS && cols % F8_ELEMS == 0) {
-      // 16 elements of one row, inside one 32-column panel
+    if (!TRANS && cols % PE == 0) {
+      // PE elements of one row, inside one 32-column panel
       const int64_t r = e0 / cols, c = e0 % cols;
-      Vec8<TX>::store(x + TX::xoff(a.mp, a.np, r, c), xv);
-      Vec8<TX>::store(x + TX::xoff(a.mp, a.np, r, c + 8), xv + 8);
+#pragma unroll
+      for (int h = 0; h < PE / 8; ++h) Vec8<TX>::store(x + TX::xoff(a.mp, a.np, r, c + 8 * h), xv + 8 * h);
     } else {
 #pragma unroll
-      for (int k = 0; k < F8_ELEMS; ++k) {
+      for (int k = 0; k < PE; ++k) {
         const int64_t r = (e0 + k) / cols, c = (e0 + k) % cols;
         TX::store(x, TRANS ? TX::xoff(a.mp, a.np, c, r) : TX::xoff(a.mp, a.np, r, c), xv[k]);
       }
@@ -152,9 +160,10 @@ __global__ __launch_bounds__(F8_NT) void fp8_pack_rows_kernel(PackArgs a, const 
 
 // rows > cols, cols % 128 == 0: a workgroup owns F8T_ROWS block rows x 128
 // block columns (one group per row) and writes the transposed X tile through
-// LDS: X rows c0 .. c0+127, columns r0 .. r0+31 (32-B runs per thread).
-constexpr int F8T_ROWS = F8_GPW;
-static_assert(F8T_ROWS == 32, "one X panel per tile");
+// LDS: X rows c0 .. c0+127, columns r0 .. r0+F8T_ROWS-1 (one 64-B panel row
+// per thread and half).
+constexpr int F8T_ROWS = P_GPW;
+static_assert(F8T_ROWS == 64, "two X panels per tile");
 template <class TG, class TX>
 __global__ __launch_bounds__(F8_NT) void fp8_pack_cols_kernel(PackArgs a, const mmuon_block_fp8* meta,
                                                               int rows, int cols, int have_state) {
@@ -163,40 +172,40 @@ __global__ __launch_bounds__(F8_NT) void fp8_pack_cols_kernel(PackArgs a, const 
   const int b = blockIdx.y;
   const int tiles_c = cols / 128;
   const int r0 = (blockIdx.x / tiles_c) * F8T_ROWS, c0 = (blockIdx.x % tiles_c) * 128;
-  const int sub = threadIdx.x % F8_LANES, rl = threadIdx.x / F8_LANES, r = r0 + rl;
+  const int sub = threadIdx.x % PL, rl = threadIdx.x / PL, r = r0 + rl;
   const mmuon_block_ref ref = a.blocks[b];
   const mmuon_block_fp8 md = meta[b];
   const auto* g = reinterpret_cast<const typename TG::storage*>(ref.grad);
   uint8_t* q = reinterpret_cast<uint8_t*>(ref.buf);
   auto* x = reinterpret_cast<typename TX::storage*>(a.x) + int64_t(b) * a.mp * a.np;
-  float nv[F8_ELEMS];
+  float nv[PE];
 #pragma unroll
-  for (int k = 0; k < F8_ELEMS; ++k) nv[k] = 0.f;
+  for (int k = 0; k < PE; ++k) nv[k] = 0.f;
   if (r < rows) {  // uniform over the group's lanes
-    const int64_t e0 = int64_t(r) * cols + c0 + sub * F8_ELEMS;
+    const int64_t e0 = int64_t(r) * cols + c0 + sub * PE;
     const int64_t grp = e0 >> 7;
     fp8_momentum_lane<TG>(q, md.scale, md.expand, md.sqrt_minmax, grp, e0, g, a.gscale, a.mu, have_state, nv);
     fp8_store_group(q, md, grp, e0, nv);
   }
 #pragma unroll
-  for (int k = 0; k < F8_ELEMS; k += 4) {
-    float4* t4 = reinterpret_cast<float4*>(&tile[rl][sub * F8_ELEMS + k]);
+  for (int k = 0; k < PE; k += 4) {
+    float4* t4 = reinterpret_cast<float4*>(&tile[rl][sub * PE + k]);
     *t4 = make_float4(TX::round(nv[k]), TX::round(nv[k + 1]), TX::round(nv[k + 2]), TX::round(nv[k + 3]));
   }
   __syncthreads();
-  // X row c0 + t/2, columns r0 + 16 (t%2) .. +15
+  // X row c0 + t/2, columns r0 + 32 (t%2) .. +31 (padding columns hold zeros)
   float ss = 0.f;
   {
-    const int cl = threadIdx.x >> 1, half = (threadIdx.x & 1) * 16;
+    const int cl = threadIdx.x >> 1, half = (threadIdx.x & 1) * 32;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < 4; ++h) {
       float v[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         v[k] = tile[half + h * 8 + k][cl];
         ss += v[k] * v[k];
       }
-      Vec8<TX>::store(x + TX::xoff(a.mp, a.np, c0 + cl, r0 + half + h * 8), v);
+      if (r0 + half + h * 8 < a.np) Vec8<TX>::store(x + TX::xoff(a.mp, a.np, c0 + cl, r0 + half + h * 8), v);
     }
   }
   const float tot = block_sum<F8_NT>(ss, red);
@@ -218,7 +227,7 @@ __global__ __launch_bounds__(256) void zero_pads_kernel(void* xv, int m, int n, 
 int fp8_pack_nparts(int rows, int cols, bool transposed) {
   if (transposed && cols % 128 == 0) return ((rows + F8T_ROWS - 1) / F8T_ROWS) * (cols / 128);
   const int64_t gpb = int64_t(rows) * cols / 128;
-  return int((gpb + F8_GPW - 1) / F8_GPW);
+  return int((gpb + P_GPW - 1) / P_GPW);
 }
 
 int launch_fp8_pack(const PackArgs& a, const mmuon_block_fp8* meta, int rows, int cols,

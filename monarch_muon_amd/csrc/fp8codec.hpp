@@ -3,7 +3,7 @@
 // Device restatement of the codec of coat_state_muon.py:22-91 (itself the
 // first/second-order half of COAT's AdamW expand kernel).  Each group of 128
 // consecutive elements carries fp32 scale, expand and sqrt_minmax.  A group is
-// held by 8 lanes, 16 consecutive elements per lane.
+// held by a few lanes of a wave, a run of consecutive elements per lane.
 #pragma once
 
 #include "common.hpp"
@@ -65,27 +65,17 @@ __device__ __forceinline__ float fp8_dequant(uint32_t code, const Fp8Meta& md, b
 }
 
 // ---------------------------------------------------------------------------
-// A group of 128 is held by F8_LANES lanes, F8_ELEMS consecutive elements per
-// lane (16 codes = one 16-byte access).  gfx950's v_cvt_f32_fp8 /
+// A group of 128 is held by 128/E lanes, E consecutive elements per lane (E a
+// multiple of 16: whole 16-byte code accesses).  gfx950's v_cvt_f32_fp8 /
 // v_cvt_pk_fp8_f32 convert OCP e4m3fn with round-to-nearest-even (the rounding
 // torch's float8_e4m3fn cast uses); the encoder's inputs are clamped to +-448
 // first, as the codec saturates.
 // ---------------------------------------------------------------------------
-constexpr int F8_ELEMS = 16;
-constexpr int F8_LANES = 128 / F8_ELEMS;
-static_assert(F8_LANES == 8, "the cross-lane reductions below span 8 lanes");
-
 __device__ __forceinline__ void e4m3_decode4(uint32_t c, float* v) {
   v[0] = __builtin_amdgcn_cvt_f32_fp8(int(c), 0);
   v[1] = __builtin_amdgcn_cvt_f32_fp8(int(c), 1);
   v[2] = __builtin_amdgcn_cvt_f32_fp8(int(c), 2);
   v[3] = __builtin_amdgcn_cvt_f32_fp8(int(c), 3);
-}
-__device__ __forceinline__ void e4m3_decode16(uint4 c, float v[16]) {
-  e4m3_decode4(c.x, v);
-  e4m3_decode4(c.y, v + 4);
-  e4m3_decode4(c.z, v + 8);
-  e4m3_decode4(c.w, v + 12);
 }
 // values already clamped to [-448, 448]
 __device__ __forceinline__ uint32_t e4m3_encode4(const float* v) {
@@ -93,33 +83,44 @@ __device__ __forceinline__ uint32_t e4m3_encode4(const float* v) {
   w = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], w, true);
   return uint32_t(w);
 }
-__device__ __forceinline__ uint4 e4m3_encode16(const float v[16]) {
-  return make_uint4(e4m3_encode4(v), e4m3_encode4(v + 4), e4m3_encode4(v + 8), e4m3_encode4(v + 12));
-}
 
-// Cross-lane max / min over the 8 lanes of a group (every lane of the group
-// active): swap neighbours, swap pairs, mirror the halves of 8.
+// Cross-lane max / min over the 128/E lanes of a group (every lane of the
+// group active): swap neighbours, swap pairs (, mirror the halves of 8).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
 }
+template <int LANES>
 __device__ __forceinline__ float group_max(float v) {
-  v = fmaxf(v, dpp_f<0xb1>(v));          // quad_perm [1,0,3,2]
-  v = fmaxf(v, dpp_f<0x4e>(v));          // quad_perm [2,3,0,1]
-  return fmaxf(v, dpp_f<0x141>(v));      // row_half_mirror
+  static_assert(LANES == 4 || LANES == 8, "groups of 4 or 8 lanes");
+  v = fmaxf(v, dpp_f<0xb1>(v));                      // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f<0x4e>(v));                      // quad_perm [2,3,0,1]
+  if constexpr (LANES == 8) v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+  return v;
 }
+template <int LANES>
 __device__ __forceinline__ float group_min(float v) {
+  static_assert(LANES == 4 || LANES == 8, "groups of 4 or 8 lanes");
   v = fminf(v, dpp_f<0xb1>(v));
   v = fminf(v, dpp_f<0x4e>(v));
-  return fminf(v, dpp_f<0x141>(v));
+  if constexpr (LANES == 8) v = fminf(v, dpp_f<0x141>(v));
+  return v;
 }
 
-// coat_state_muon.py:22-43 for this lane's 16 elements of one group.
-__device__ __forceinline__ void fp8_dequant16(uint4 codes, const Fp8Dq& d, bool sgn, float out[16]) {
-  float raw[16];
-  e4m3_decode16(codes, raw);
+// coat_state_muon.py:22-43 for this lane's E elements of one group.
+template <int E>
+__device__ __forceinline__ void fp8_dequant_lane(const uint4 (&codes)[E / 16], const Fp8Dq& d, bool sgn,
+                                                 float (&out)[E]) {
+  float raw[E];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
+  for (int h = 0; h < E / 16; ++h) {
+    e4m3_decode4(codes[h].x, raw + 16 * h);
+    e4m3_decode4(codes[h].y, raw + 16 * h + 4);
+    e4m3_decode4(codes[h].z, raw + 16 * h + 8);
+    e4m3_decode4(codes[h].w, raw + 16 * h + 12);
+  }
+#pragma unroll
+  for (int k = 0; k < E; ++k) {
     if (sgn) {
       const float scaled = raw[k] * d.scale;
       const float absolute = fabsf(scaled);
@@ -135,21 +136,22 @@ __device__ __forceinline__ void fp8_dequant16(uint4 codes, const Fp8Dq& d, bool 
 
 // coat_state_muon.py:46-91 for one group (nvalid: this lane's elements that
 // exist).  Returns the group metadata (valid in every lane of the group) and
-// this lane's 16 codes.  The normalised value is multiplied by 1/scale rather
+// this lane's E codes.  The normalised value is multiplied by 1/scale rather
 // than divided by scale, and scale's power uses pow_pos (both visible only at
 // e4m3 rounding ties).
-__device__ __forceinline__ Fp8Meta fp8_quant_group(const float x[16], int nvalid, bool sgn, uint4& codes) {
+template <int E>
+__device__ __forceinline__ Fp8Meta fp8_quant_group(const float (&x)[E], int nvalid, bool sgn, uint4 (&codes)[E / 16]) {
   float amax = 0.f, amin = 3.4028235e38f;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
+  for (int k = 0; k < E; ++k) {
     const float a = fabsf(x[k]);
     if (k < nvalid) {
       amax = fmaxf(amax, a);
       if (a > 0.f) amin = fminf(amin, a);
     }
   }
-  amax = fmaxf(group_max(amax), QEPS);
-  amin = group_min(amin);
+  amax = fmaxf(group_max<128 / E>(amax), QEPS);
+  amin = group_min<128 / E>(amin);
   amin = amin < 3.4028235e38f ? fmaxf(amin, QEPS) : QEPS;  // no non-zero value: QEPS
   float ratio = amax / amin;
   ratio = fmaxf(ratio, 1.0f + QEPS);
@@ -161,16 +163,19 @@ __device__ __forceinline__ Fp8Meta fp8_quant_group(const float x[16], int nvalid
   const float smm = fmaxf(sqrtf(amax) * sqrtf(amin), QEPS);
   const float scale = fmaxf(pow_pos(fmaxf(amax / smm, QEPS), expand) / FP8_MAX, QEPS);
   const float inv_smm = 1.0f / smm, inv_scale = 1.0f / scale;
-  float y[16];
+  float y[E];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
+  for (int k = 0; k < E; ++k) {
     const float a = fabsf(x[k]);
     const float np = pow_pos(fmaxf(a * inv_smm, QEPS), expand);
     float nrm = 0.f;
     if (k < nvalid && a > 0.f) nrm = sgn ? copysignf(np, x[k]) : np;
     y[k] = __builtin_amdgcn_fmed3f(nrm * inv_scale, -FP8_MAX, FP8_MAX);
   }
-  codes = e4m3_encode16(y);
+#pragma unroll
+  for (int h = 0; h < E / 16; ++h)
+    codes[h] = make_uint4(e4m3_encode4(y + 16 * h), e4m3_encode4(y + 16 * h + 4), e4m3_encode4(y + 16 * h + 8),
+                          e4m3_encode4(y + 16 * h + 12));
   return Fp8Meta{scale, expand, smm};
 }
 
