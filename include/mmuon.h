@@ -1,6 +1,7 @@
 /*
  * mmuon.h -- C ABI of libmmuon.so, the MI355X (gfx950) implementation of the
- * Monarch-Muon optimizer step.
+ * Monarch-Muon optimizer step (and of the Monarch butterfly multiply whose
+ * backward produces the gradients the step consumes).
  *
  * The reference has no native boundary on this path: its step is a sequence
  * of torch ops (membench/src/models/monarch/monarch_muon.py:140-208,
@@ -229,6 +230,50 @@ typedef struct mmuon_grad_norm_args {
   float* coef;                       /* device, 1 float (out) */
 } mmuon_grad_norm_args;
 int mmuon_grad_clip_coef(const mmuon_grad_norm_args* a, void* stream);
+
+/* Monarch butterfly multiply, the layer step that produces the (nb, r, c)
+   gradients the optimizer consumes.  w1 (nblocks, q, p) and w2 (nblocks, s, q)
+   are a MonarchLinear's blkdiag1 / blkdiag2 (k = l = nblocks, r = q);
+   x (tokens, nblocks * p) its padded input.  bf16 throughout, fp32
+   accumulation, every product rounded to bf16 as the reference's bmms round.
+     out1[ll][b][i]  = riffle of x[b][kk] . w1[kk]^T  (nblocks, tokens, q),
+                       the intermediate saved for the backward;
+     out[b][ll][j]   = out1[ll][b] . w2[ll][j]       (tokens, nblocks, s),
+                       the blocked output (the caller's view
+                       out.transpose(1, 2).reshape(tokens, s * nblocks) is the
+                       layer's feature order).
+   Requirements: p, q, s multiples of 8; q / nblocks a multiple of 32;
+   nblocks in {1, 2, 4, 8, 16}; 1 <= tokens < 2^24 (0 allowed); every pointer
+   16-B aligned, tensors contiguous.  The tensors must not overlap. */
+typedef struct mmuon_butterfly_args {
+  int64_t tokens;
+  int32_t nblocks;
+  int32_t q, p, s;
+  int32_t dtype;          /* MMUON_BF16 */
+  const void* x;          /* (tokens, nblocks * p)   */
+  const void* w1;         /* (nblocks, q, p)         */
+  const void* w2;         /* (nblocks, s, q)         */
+  void* out;              /* forward out: (tokens, nblocks, s)  */
+  void* out1;             /* forward out / backward in: (nblocks, tokens, q) */
+  const void* dout;       /* backward in: (tokens, nblocks, s)  */
+  void* dx;               /* backward out: (tokens, nblocks * p) */
+  void* dw1;              /* backward out: (nblocks, q, p) */
+  void* dw2;              /* backward out: (nblocks, s, q) */
+  void* workspace;        /* backward: mmuon_butterfly_workspace() bytes, 256-B aligned */
+  size_t workspace_bytes;
+} mmuon_butterfly_args;
+/* Forward.  Replaces pretrain/src/models/monarch/monarch_ops.py:23-46
+   (_butterfly_fwd_blocked / monarch::butterfly_blk: two bmms with the riffle of
+   monarch_riffle.py:13-57 between them); out1 is written in riffled order by
+   the first product, so no separate riffle pass runs. */
+int mmuon_butterfly_fwd(const mmuon_butterfly_args* a, void* stream);
+/* Backward: dx, dw1, dw2 from x, w1, w2, out1 and dout.  Replaces
+   pretrain/src/models/monarch/monarch_ops.py:57-82 (monarch::butterfly_blk_bwd:
+   four bmms and the unriffle of monarch_riffle.py:60-107); the unriffle is
+   folded into the addressing of the products that read it. */
+int mmuon_butterfly_bwd(const mmuon_butterfly_args* a, void* stream);
+/* Workspace bytes the backward needs for these shapes (x, pointers unused). */
+size_t mmuon_butterfly_workspace(const mmuon_butterfly_args* a);
 
 /* Thread-local message of the last failing call ("" if none). */
 const char* mmuon_last_error(void);

@@ -16,7 +16,7 @@ LIB_PATH = Path(os.environ.get("MMUON_LIB", Path(__file__).resolve().parent / "l
 F32, BF16, F8E4M3 = 0, 1, 2
 GROUP_ALIGNED16 = 1
 NS_NO_APPLY = 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8E4M3}
 
@@ -82,6 +82,14 @@ class GradNormArgs(C.Structure):
                 ("norms", C.c_void_p), ("total", C.c_void_p), ("coef", C.c_void_p)]
 
 
+class ButterflyArgs(C.Structure):
+    _fields_ = [("tokens", C.c_int64), ("nblocks", C.c_int32), ("q", C.c_int32), ("p", C.c_int32),
+                ("s", C.c_int32), ("dtype", C.c_int32),
+                ("x", C.c_void_p), ("w1", C.c_void_p), ("w2", C.c_void_p), ("out", C.c_void_p),
+                ("out1", C.c_void_p), ("dout", C.c_void_p), ("dx", C.c_void_p), ("dw1", C.c_void_p),
+                ("dw2", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
+
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "mmuon_abi_version": (C.c_int, []),
@@ -101,6 +109,9 @@ SIGNATURES = {
     "mmuon_fp8_dequantize": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                        C.c_int64, C.c_int32, C.c_void_p]),
     "mmuon_grad_clip_coef": (C.c_int, [C.POINTER(GradNormArgs), C.c_void_p]),
+    "mmuon_butterfly_fwd": (C.c_int, [C.POINTER(ButterflyArgs), C.c_void_p]),
+    "mmuon_butterfly_bwd": (C.c_int, [C.POINTER(ButterflyArgs), C.c_void_p]),
+    "mmuon_butterfly_workspace": (C.c_size_t, [C.POINTER(ButterflyArgs)]),
 }
 
 _lib = None

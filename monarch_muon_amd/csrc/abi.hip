@@ -107,7 +107,7 @@ extern "C" {
 
 const char* mmuon_last_error(void) { return g_err.c_str(); }
 
-int mmuon_abi_version(void) { return 2; }
+int mmuon_abi_version(void) { return 3; }
 
 int mmuon_ns_layout(int32_t rows, int32_t cols, int32_t ns_dtype, int64_t nblocks,
                     mmuon_ns_layout_t* out) {
@@ -339,6 +339,71 @@ int mmuon_grad_clip_coef(const mmuon_grad_norm_args* a, void* stream) {
     return fail(MMUON_EINVAL, "null gradient-norm pointer");
   mmuon::launch_grad_clip_coef(*a, static_cast<hipStream_t>(stream));
   return check_launch("mmuon_grad_clip_coef");
+}
+
+}  // extern "C"
+
+namespace {
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int check_butterfly(const mmuon_butterfly_args* a, bool bwd) {
+  if (a == nullptr) return fail(MMUON_EINVAL, "null butterfly arguments");
+  if (a->dtype != MMUON_BF16) return fail(MMUON_EINVAL, "butterfly: dtype must be MMUON_BF16 (got %d)", a->dtype);
+  const int nb = a->nblocks;
+  if (nb != 1 && nb != 2 && nb != 4 && nb != 8 && nb != 16)
+    return fail(MMUON_EINVAL, "butterfly: nblocks must be 1, 2, 4, 8 or 16 (got %d)", nb);
+  if (a->q <= 0 || a->p <= 0 || a->s <= 0 || a->q % 8 || a->p % 8 || a->s % 8)
+    return fail(MMUON_EINVAL, "butterfly: block sides must be positive multiples of 8 (q %d, p %d, s %d)", a->q, a->p,
+                a->s);
+  if ((a->q / nb) % 32 != 0 || a->q % nb != 0)
+    return fail(MMUON_EINVAL, "butterfly: q / nblocks must be a multiple of 32 (q %d, nblocks %d)", a->q, nb);
+  if (a->q >= (1 << 16) || a->p >= (1 << 16) || a->s >= (1 << 16))
+    return fail(MMUON_ERANGE, "butterfly: block sides beyond 65535");
+  if (a->tokens < 0 || a->tokens >= (int64_t(1) << 24))
+    return fail(MMUON_ERANGE, "butterfly: tokens must be in [0, 2^24) (got %lld)", (long long)a->tokens);
+  // per-lane offsets of a tile stay below 2^31: 256 rows of x, dout or out1
+  // and 32 token rows x the planes of the intermediate
+  const int64_t pitch = int64_t(std::max({nb * a->p, nb * a->s, a->q})) * 2;
+  if (256 * pitch >= (int64_t(1) << 31) || int64_t(nb) * a->tokens * a->q * 2 >= (int64_t(1) << 31))
+    return fail(MMUON_ERANGE, "butterfly: tensors beyond the kernels' 32-bit tile offsets");
+  const void* in[] = {a->x, a->w1, a->w2, a->out1};
+  for (const void* p : in)
+    if (p == nullptr || !aligned16(p)) return fail(MMUON_EINVAL, "butterfly: null or unaligned input pointer");
+  if (!bwd) {
+    if (a->out == nullptr || !aligned16(a->out)) return fail(MMUON_EINVAL, "butterfly: null or unaligned out");
+    return MMUON_OK;
+  }
+  const void* bw[] = {a->dout, a->dx, a->dw1, a->dw2, a->workspace};
+  for (const void* p : bw)
+    if (p == nullptr || !aligned16(p)) return fail(MMUON_EINVAL, "butterfly: null or unaligned backward pointer");
+  if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0)
+    return fail(MMUON_EINVAL, "butterfly: workspace must be 256-B aligned");
+  if (a->workspace_bytes < mmuon::butterfly_workspace(*a))
+    return fail(MMUON_EINVAL, "butterfly: workspace of %zu bytes, %zu needed", a->workspace_bytes,
+                mmuon::butterfly_workspace(*a));
+  return MMUON_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mmuon_butterfly_workspace(const mmuon_butterfly_args* a) {
+  if (a == nullptr || a->nblocks <= 0 || a->q <= 0 || a->p <= 0 || a->s <= 0 || a->tokens < 0) return 0;
+  return mmuon::butterfly_workspace(*a);
+}
+
+int mmuon_butterfly_fwd(const mmuon_butterfly_args* a, void* stream) {
+  if (int rc = check_butterfly(a, false)) return rc;
+  mmuon::launch_butterfly_fwd(*a, static_cast<hipStream_t>(stream));
+  return check_launch("butterfly forward");
+}
+
+int mmuon_butterfly_bwd(const mmuon_butterfly_args* a, void* stream) {
+  if (int rc = check_butterfly(a, true)) return rc;
+  mmuon::launch_butterfly_bwd(*a, static_cast<hipStream_t>(stream));
+  return check_launch("butterfly backward");
 }
 
 }  // extern "C"

@@ -73,6 +73,11 @@ int launch_adamw_fp8(const AdamWArgs& a, int param_dtype, int grad_dtype, hipStr
 // Gradient-norm clipping coefficient --------------------------------------------
 int launch_grad_clip_coef(const mmuon_grad_norm_args& a, hipStream_t s);
 
+// Monarch butterfly multiply -------------------------------------------------------
+size_t butterfly_workspace(const mmuon_butterfly_args& a);
+int launch_butterfly_fwd(const mmuon_butterfly_args& a, hipStream_t s);
+int launch_butterfly_bwd(const mmuon_butterfly_args& a, hipStream_t s);
+
 // Gradient as the step reads it: dtype(g * c) when clipping, else g.
 template <class TG>
 __device__ __forceinline__ float clipped(float g, const float* gscale) {

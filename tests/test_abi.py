@@ -32,7 +32,8 @@ def test_struct_layouts_match_header(tmp_path):
     structs = {"mmuon_block_ref": _abi.BlockRef, "mmuon_block_fp8": _abi.BlockFp8,
                "mmuon_ns_layout_t": _abi.NsLayout, "mmuon_group": _abi.Group,
                "mmuon_adamw_tensor": _abi.AdamWTensor, "mmuon_adamw_args": _abi.AdamWArgs,
-               "mmuon_adamw_fp8_tensor": _abi.AdamWFp8Tensor}
+               "mmuon_adamw_fp8_tensor": _abi.AdamWFp8Tensor, "mmuon_grad_tensor": _abi.GradTensor,
+               "mmuon_grad_norm_args": _abi.GradNormArgs, "mmuon_butterfly_args": _abi.ButterflyArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -91,3 +92,34 @@ def test_product_path_refuses_cpu_tensors():
     opt = MonarchMuonOptimizer([p], [])
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         opt.step()
+
+
+def test_butterfly_entry_points_validate_before_launching():
+    """Every descriptor here is invalid, so no kernel is launched (no GPU needed)."""
+    lib = _abi.lib()
+    a = _abi.ButterflyArgs(tokens=16, nblocks=4, q=64, p=64, s=64, dtype=_abi.BF16,
+                           x=4096, w1=8192, w2=12288, out=16384, out1=20480)
+    assert lib.mmuon_butterfly_fwd(None, None) == -1
+    assert lib.mmuon_butterfly_fwd(C.byref(a), None) == -1           # q / nblocks = 16
+    assert b"multiple of 32" in lib.mmuon_last_error()
+    a.q, a.dtype = 128, _abi.F32
+    assert lib.mmuon_butterfly_fwd(C.byref(a), None) == -1
+    assert b"MMUON_BF16" in lib.mmuon_last_error()
+    a.dtype, a.nblocks = _abi.BF16, 3
+    assert lib.mmuon_butterfly_fwd(C.byref(a), None) == -1
+    assert b"nblocks" in lib.mmuon_last_error()
+    a.nblocks, a.p = 4, 60
+    assert lib.mmuon_butterfly_fwd(C.byref(a), None) == -1
+    assert b"multiples of 8" in lib.mmuon_last_error()
+    a.p, a.x = 64, 4100
+    assert lib.mmuon_butterfly_fwd(C.byref(a), None) == -1
+    assert b"unaligned" in lib.mmuon_last_error()
+    a.x, a.tokens = 4096, 1 << 24
+    assert lib.mmuon_butterfly_fwd(C.byref(a), None) == -3
+    a.tokens = 16
+    # backward: dout, dx, dw1, dw2 present, workspace too small
+    a.dout, a.dx, a.dw1, a.dw2, a.workspace, a.workspace_bytes = 24576, 28672, 32768, 36864, 40960, 16
+    need = lib.mmuon_butterfly_workspace(C.byref(a))
+    assert need >= 4 * 16 * 128 * 2
+    assert lib.mmuon_butterfly_bwd(C.byref(a), None) == -1
+    assert b"workspace" in lib.mmuon_last_error()
