@@ -367,16 +367,18 @@ int check_butterfly(const mmuon_butterfly_args* a, bool bwd) {
   const int64_t pitch = int64_t(std::max({nb * a->p, nb * a->s, a->q})) * 2;
   if (256 * pitch >= (int64_t(1) << 31) || int64_t(nb) * a->tokens * a->q * 2 >= (int64_t(1) << 31))
     return fail(MMUON_ERANGE, "butterfly: tensors beyond the kernels' 32-bit tile offsets");
-  const void* in[] = {a->x, a->w1, a->w2, a->out1};
-  for (const void* p : in)
-    if (p == nullptr || !aligned16(p)) return fail(MMUON_EINVAL, "butterfly: null or unaligned input pointer");
+  // token-sized tensors may be empty (null) when tokens == 0
+  auto bad = [&](const void* p, bool per_token) {
+    return (p == nullptr && !(per_token && a->tokens == 0)) || !aligned16(p);
+  };
+  if (bad(a->w1, false) || bad(a->w2, false) || bad(a->x, true) || bad(a->out1, true))
+    return fail(MMUON_EINVAL, "butterfly: null or unaligned input pointer");
   if (!bwd) {
-    if (a->out == nullptr || !aligned16(a->out)) return fail(MMUON_EINVAL, "butterfly: null or unaligned out");
+    if (bad(a->out, true)) return fail(MMUON_EINVAL, "butterfly: null or unaligned out");
     return MMUON_OK;
   }
-  const void* bw[] = {a->dout, a->dx, a->dw1, a->dw2, a->workspace};
-  for (const void* p : bw)
-    if (p == nullptr || !aligned16(p)) return fail(MMUON_EINVAL, "butterfly: null or unaligned backward pointer");
+  if (bad(a->dout, true) || bad(a->dx, true) || bad(a->dw1, false) || bad(a->dw2, false) || bad(a->workspace, false))
+    return fail(MMUON_EINVAL, "butterfly: null or unaligned backward pointer");
   if ((reinterpret_cast<uintptr_t>(a->workspace) & 255) != 0)
     return fail(MMUON_EINVAL, "butterfly: workspace must be 256-B aligned");
   if (a->workspace_bytes < mmuon::butterfly_workspace(*a))

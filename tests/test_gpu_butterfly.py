@@ -4,11 +4,11 @@ oracle (oracle/butterfly.py, pinned by tests/test_oracle_butterfly.py).
 Inputs are bf16, the oracle multiplies the same bf16 values in fp32 and rounds each product to
 bf16 where the reference's bmms round.  Only the summation order differs, so an output element
 differs by at most a bf16 rounding step where the fp32 sums straddle one.  Bar: relative Frobenius
-error <= 1e-2 per output (the bf16 tolerance of the optimizer path); the measured errors are
-printed and sit near 1e-3.  Shapes: the Monarch factors of the benchmark models (toy nb=2,
-257M nb=2, 1.3B nb=4, 6.89B nb=4: square, tall-w2 and wide-w1 layers), token counts that are
-not multiples of the 256-row tile, split-K weight gradients with a ragged last split, and the
-empty and single-token edge cases.
+error <= 2e-3 per output, five times tighter than the bf16 tolerance of the optimizer path (1e-2);
+the measured errors are printed and sit between 2e-5 and 2e-4.  Shapes: the Monarch factors of
+the benchmark models (toy nb=2, 257M nb=2, 1.3B nb=4, 6.89B nb=4: square, tall-w2 and wide-w1
+layers), token counts that are not multiples of the 256-row tile, split-K weight gradients with a
+ragged last split, and the empty and single-token edge cases.
 """
 import pytest
 import torch
@@ -19,7 +19,7 @@ from oracle.truth import rel_fro
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
-TOL = 1e-2
+TOL = 2e-3
 
 # (tokens, nblocks, q, p, s): w1 (nb, q, p), w2 (nb, s, q), x (tokens, nb p)
 CASES = [
