@@ -1,6 +1,7 @@
 """Monarch-Muon optimizer-step benchmark on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--workload 6.89b-nb4] [--no-cpu-baseline]
+    python bench.py --workload butterfly-6.89b [--tokens 4096]
 
 Runs the full ``MonarchMuonOptimizer.step()`` (Muon group: momentum, bf16
 Newton-Schulz over every Monarch block, apply; AdamW group) of the named
@@ -9,6 +10,12 @@ between two device synchronisations, and prints one JSON line.  The dominant
 kernel's roofline comes from per-launch hipEvents on the launch stream over
 extra instrumented steps; the CPU baseline times the oracle (the CPU
 restatement of the reference step) on a bounded sample of the same workload.
+
+``--workload butterfly-<model>`` times the Monarch butterfly multiply instead:
+forward + backward of one transformer layer's seven Monarch projections
+(q, k, v, o, gate, up, down) at ``--tokens`` rows (default 4096, the reference
+benchmark's micro-batch 4 x sequence 1024), beside the reference's own torch
+ops for the same layer run on the same GPU.
 """
 from __future__ import annotations
 
@@ -226,6 +233,171 @@ def cpu_baseline(w, seed=0):
             "cpu_model": model, "os_cpu_count": os.cpu_count()}
 
 
+# ---------------------------------------------------------------- butterfly
+BUTTERFLY_METRIC = "Monarch layer fwd+bwd ms (7 butterfly projections), bf16; TFLOP/s as % of bf16 MFMA peak"
+
+
+def butterfly_layer(w, tokens, device, seed=0):
+    """The seven Monarch projections of one layer: [(name, x, w1, w2, dout)], bf16."""
+    from monarch_muon_amd.workloads import factor_shapes, mlp_hidden
+    hid = mlp_hidden(w.n_embd, w.intermediate)
+    dims = [("q", w.n_embd, w.n_embd), ("k", w.n_embd, w.n_embd), ("v", w.n_embd, w.n_embd),
+            ("o", w.n_embd, w.n_embd), ("gate", w.n_embd, hid), ("up", w.n_embd, hid), ("down", hid, w.n_embd)]
+    g = torch.Generator(device=device).manual_seed(seed)
+    out = []
+    for name, d_in, d_out in dims:
+        s1, s2 = factor_shapes(d_in, d_out, w.nblocks)
+        x = torch.randn(tokens, s1[0] * s1[2], device=device, generator=g).bfloat16()
+        w1 = (torch.randn(*s1, device=device, generator=g) / s1[2] ** 0.5).bfloat16()
+        w2 = (torch.randn(*s2, device=device, generator=g) / s2[2] ** 0.5).bfloat16()
+        dout = torch.randn(tokens, s2[0], s2[1], device=device, generator=g).bfloat16()
+        out.append((name, x, w1, w2, dout))
+    return out
+
+
+def butterfly_flops(x, w1, w2):
+    """Forward flops of one projection (two batched products); the backward is twice this."""
+    k, q, p = w1.shape
+    l, s, r = w2.shape
+    return 2 * x.shape[0] * (k * q * p + l * s * r)
+
+
+def torch_reference_fwd(x2, w1, w2):
+    """pretrain/src/models/monarch/monarch_ops.py:23-36 with the eager riffle (right operands made
+    contiguous: transposed bf16 bmm operands are avoided on this platform)."""
+    B = x2.shape[0]
+    k, q, p = w1.shape
+    l, s, r = w2.shape
+    out1 = torch.bmm(x2.reshape(B, k, p).transpose(0, 1), w1.transpose(-1, -2).contiguous())
+    t = out1.transpose(0, 1).reshape(B, r, l).permute(2, 0, 1).contiguous()
+    return torch.bmm(t, w2.transpose(-1, -2).contiguous()).transpose(0, 1).contiguous(), t
+
+
+def torch_reference_bwd(x2, w1, w2, out1, dout_blk):
+    """monarch_ops.py:57-82 with the eager unriffle."""
+    B = x2.shape[0]
+    k, q, p = w1.shape
+    l, s, r = w2.shape
+    d = dout_blk.permute(1, 0, 2)
+    dw2 = torch.bmm(d.transpose(-1, -2).contiguous(), out1)
+    dt = torch.bmm(d.contiguous(), w2)
+    dout1 = dt.transpose(0, 1).transpose(-1, -2).contiguous().reshape(B, k, q).transpose(0, 1).contiguous()
+    dx = torch.bmm(dout1, w1).transpose(0, 1).reshape(B, k * p)
+    dw1 = torch.bmm(dout1.transpose(-1, -2).contiguous(), x2.reshape(B, k, p).transpose(0, 1).contiguous())
+    return dx, dw1, dw2
+
+
+def butterfly_cpu_baseline(layer):
+    """The oracle (torch CPU) forward + backward of every projection of the layer at 1/8 of the
+    tokens, scaled by 8."""
+    from oracle import butterfly as bf
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    frac = 8
+    cpu = [(x[: x.shape[0] // frac].cpu(), w1.cpu(), w2.cpu(), d[: d.shape[0] // frac].cpu())
+           for _, x, w1, w2, d in layer]
+
+    def run():
+        for x, w1, w2, d in cpu:
+            _, o1 = bf.butterfly_fwd(x, w1, w2)
+            bf.butterfly_bwd(x, w1, w2, o1, d)
+
+    run()
+    t0 = time.perf_counter()
+    run()
+    sample_ms = (time.perf_counter() - t0) * 1e3
+    return {"value": round(sample_ms * frac, 1), "unit": "ms", "cores": threads, "kind": "port",
+            "sample": f"oracle butterfly fwd+bwd (torch CPU, fp32 products of bf16 values) of the 7 projections "
+                      f"at {cpu[0][0].shape[0]} tokens = {sample_ms:.1f} ms after 1 warm-up, x{frac}",
+            "os_cpu_count": os.cpu_count()}
+
+
+def bench_butterfly(args, w):
+    from monarch_muon_amd import butterfly_blk_bwd_op, butterfly_blk_op
+    dev = torch.device("cuda", 0)
+    tokens = args.tokens
+    log(f"[bench] butterfly layer of {w.name}, {tokens} tokens, on {torch.cuda.get_device_name(dev)}")
+    layer = butterfly_layer(w, tokens, dev)
+    fwd_fl = sum(butterfly_flops(x, w1, w2) for _, x, w1, w2, _ in layer)
+    saved = {}
+
+    def step():
+        for name, x, w1, w2, _ in layer:
+            saved[name] = butterfly_blk_op(x, w1, w2)[1]
+        for name, x, w1, w2, d in reversed(layer):
+            butterfly_blk_bwd_op(x, w1, w2, saved[name], d)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for a, b in evs:
+        a.record()
+        step()
+        b.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ev_ms = statistics.median(a.elapsed_time(b) for a, b in evs)
+
+    # per-op times (hipEvents on the launch stream, which is torch's current stream)
+    def op_ms(fn, reps=10):
+        fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    per = {}
+    fwd_ms = bwd_ms = ref_fwd_ms = ref_bwd_ms = 0.0
+    for name, x, w1, w2, d in layer:
+        fl = butterfly_flops(x, w1, w2)
+        f = op_ms(lambda: butterfly_blk_op(x, w1, w2))
+        o1 = butterfly_blk_op(x, w1, w2)[1]
+        bw = op_ms(lambda: butterfly_blk_bwd_op(x, w1, w2, o1, d))
+        rf = op_ms(lambda: torch_reference_fwd(x, w1, w2))
+        rt = torch_reference_fwd(x, w1, w2)[1]
+        rb = op_ms(lambda: torch_reference_bwd(x, w1, w2, rt, d))
+        fwd_ms, bwd_ms, ref_fwd_ms, ref_bwd_ms = fwd_ms + f, bwd_ms + bw, ref_fwd_ms + rf, ref_bwd_ms + rb
+        per[name] = {"w1": list(w1.shape), "w2": list(w2.shape), "fwd_ms": round(f, 4), "bwd_ms": round(bw, 4),
+                     "fwd_tflops": round(fl / (f * 1e-3) / 1e12, 1), "bwd_tflops": round(2 * fl / (bw * 1e-3) / 1e12, 1),
+                     "torch_fwd_ms": round(rf, 4), "torch_bwd_ms": round(rb, 4)}
+    # the dominant kernel: the forward product (two launches of butterfly_gemm<false, false, false>
+    # per forward call; the event pair around the call also holds the gap between them)
+    fwd_avg_launch = fwd_ms / (2 * len(layer))
+    achieved = fwd_fl / (fwd_ms * 1e-3) / 1e12
+    total_fl = 3 * fwd_fl
+    res = {
+        "metric": BUTTERFLY_METRIC, "value": round(wall_ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall_ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations and gradients, N(0,1/fan_in) factors, resident in HBM)",
+        "config": {"workload": f"butterfly-{w.name.split('-')[0]}", "tokens": tokens, "nblocks": w.nblocks,
+                   "hidden": w.n_embd, "intermediate": w.intermediate, "projections": 7,
+                   "step": "forward of the 7 projections, then their backward in reverse order"},
+        "median_event_ms": round(ev_ms, 4),
+        "tflops": round(total_fl / (wall_ms * 1e-3) / 1e12, 1),
+        "frac_peak": round(total_fl / (wall_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "kernel": "butterfly_gemm<false, false, false>", "achieved": round(achieved, 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None, "avg_launch_ms": round(fwd_avg_launch, 4),
+                     "alg_flops_per_launch": fwd_fl / (2 * len(layer))},
+        "forward_ms": round(fwd_ms, 4), "backward_ms": round(bwd_ms, 4),
+        "torch_reference_ms": {"forward": round(ref_fwd_ms, 4), "backward": round(ref_bwd_ms, 4),
+                               "total": round(ref_fwd_ms + ref_bwd_ms, 4),
+                               "note": "the reference's monarch_ops.py bmm + eager riffle path, same GPU, per-op events"},
+        "projections": per,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (oracle on host cores, bounded sample)")
+        res["cpu_baseline"] = butterfly_cpu_baseline(layer)
+    print(json.dumps(res), flush=True)
+
+
 # ---------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser()
@@ -233,6 +405,7 @@ def main():
     ap.add_argument("--steps", type=int, default=12)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="6.89b-nb4")
+    ap.add_argument("--tokens", type=int, default=4096, help="butterfly workloads: rows of the layer input")
     ap.add_argument("--instrumented", type=int, default=2, help="extra per-kernel-timed steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--grad-clip", type=float, default=0.0,
@@ -253,6 +426,11 @@ def main():
               "this build (see DESIGN.md for how the step would shard).", file=sys.stderr)
         sys.exit(2)
     from monarch_muon_amd.workloads import WORKLOADS, adamw_elements, muon_elements, ns_flops
+    if args.workload.startswith("butterfly-"):
+        model = args.workload[len("butterfly-"):]
+        base = next(k for k in WORKLOADS if k.split("-")[0] == model)
+        bench_butterfly(args, WORKLOADS[base])
+        return
     w = WORKLOADS[args.workload]
     dev = torch.device("cuda", 0)
     log(f"[bench] building workload {w.name} on {torch.cuda.get_device_name(dev)}")

@@ -125,15 +125,18 @@ struct GemmArgs {
   int M, N, K, G, S;
   int kchunk;      // K per split, a multiple of BK
   int tiles_m, tiles_n;
-  int vtiles;      // virtual tiles: (G * S * tiles_m rounded up to a multiple of 8) * tiles_n
+  int vtiles;      // virtual tiles: 8 XCDs x ceil(G * S * tiles_m / 8) groups x tiles_n
 };
 
 // ---------------------------------------------------------------------------
 // The pipelined main loop (the NS kernels' schedule with both operand forms
-// fixed per launch): slice kt in ring slot kt % NSTAGE, two slices in flight
+// fixed per launch): slice kt in ring slot kt % RING, RING - 2 slices in flight
 // behind the one being read, fragment reads and buffer loads interleaved one
-// per MFMA.
+// per MFMA.  (A fifth slot, the whole LDS, measured slightly slower.)
 // ---------------------------------------------------------------------------
+constexpr int RING = 4;
+constexpr int RING_ELEMS = RING * SLOT;
+static_assert(RING_ELEMS * 2 <= 160 * 1024 && RING_ELEMS >= BN * 256, "ring and staged tile fit the LDS");
 template <bool AT, bool BT>
 struct GPipe {
   static_assert(RDMA == 2 && CDMA == 2, "two buffer loads per thread and operand slice");
@@ -148,7 +151,7 @@ struct GPipe {
   uint32_t kfrag[BK / 16];
   uint32_t tfrag_r, tfrag_c;
 
-  __device__ __forceinline__ const uint16_t* slot(int kt) const { return lds + (kt % NSTAGE) * SLOT; }
+  __device__ __forceinline__ const uint16_t* slot(int kt) const { return lds + (kt % RING) * SLOT; }
 
   // K delta of this lane's load q within a slice: K form, its 8-element chunk;
   // T form, its k row
@@ -166,7 +169,7 @@ struct GPipe {
   __device__ __forceinline__ void issue_one(int src_kt, int slot_kt) const {
     constexpr int q = Q & 1;
     constexpr bool T = Q < 2 ? AT : BT;
-    const uint32_t dst = lds0 + (slot_kt % NSTAGE) * SLOT * 2 + (Q < 2 ? 0 : RSLICE * 2) + (2 * wave + q) * 1024;
+    const uint32_t dst = lds0 + (slot_kt % RING) * SLOT * 2 + (Q < 2 ? 0 : RSLICE * 2) + (2 * wave + q) * 1024;
     const int k0 = kbeg + src_kt * BK;
     const char* sb = (Q < 2 ? abase : bbase) + k_off(Q < 2 ? ak : bk, k0);
     uint32_t voff = loff[Q];
@@ -201,10 +204,10 @@ struct GPipe {
     MMUON_GSTEP0(0) MMUON_GSTEP0(1) MMUON_GSTEP0(2) MMUON_GSTEP0(3)
     MMUON_GSTEP0(4) MMUON_GSTEP0(5) MMUON_GSTEP0(6) MMUON_GSTEP0(7)
 #undef MMUON_GSTEP0
-    wait_vm<(NSTAGE - 3) * SLICE_DMA>();  // slice kt+1 landed
+    wait_vm<(RING - 3) * SLICE_DMA>();  // slice kt+1 landed
     barrier();
-    const int src = kt + NSTAGE - 1 < KT ? kt + NSTAGE - 1 : KT - 1;
-    const int slt = kt + NSTAGE - 1;
+    const int src = kt + RING - 1 < KT ? kt + RING - 1 : KT - 1;
+    const int slt = kt + RING - 1;
 #define MMUON_GSTEP1(g)                                                                      \
     acc[(g) / TMJ][(g) % TMJ] = mfma(fb.r[(g) / TMJ], fb.c[(g) % TMJ], acc[(g) / TMJ][(g) % TMJ]); \
     if constexpr ((g) < TMI + TMJ) load_one<0, (g)>(kt + 1, fa);                             \
@@ -221,8 +224,8 @@ struct GPipe {
 #pragma unroll
       for (int j = 0; j < TMJ; ++j) acc[i][j] = f32x16{};
 #pragma unroll
-    for (int q = 0; q < NSTAGE - 1; ++q) issue(q < KT ? q : KT - 1, q);
-    wait_vm<(NSTAGE - 2) * SLICE_DMA>();  // slice 0 landed
+    for (int q = 0; q < RING - 1; ++q) issue(q < KT ? q : KT - 1, q);
+    wait_vm<(RING - 2) * SLICE_DMA>();  // slice 0 landed
     barrier();
     Frags fa, fb;
     load_one<0, 0>(0, fa);
@@ -308,14 +311,20 @@ __device__ __forceinline__ void write_tile(const char* stage, int log2l, Fn&& fn
   }
 }
 
-// Virtual tile v -> (batch g, split sp, tile row tm, tile column tn).  Groups
-// (g, sp, tm) share the row operand's slice run; the tiles_n tiles of a group
-// go to one XCD (virtual tile v runs on XCD v % 8) in consecutive rounds.
+// Virtual tile v -> (batch g, split sp, tile row tm, tile column tn).  A group
+// (g, sp, tm) is the tiles_n tiles that share a row-operand band; groups are
+// numbered tm fastest and dealt to the XCDs in contiguous runs (virtual tile v
+// runs on XCD v % 8), so the tiles of one XCD share one batch's column operand
+// and few row bands, and each operand block is fetched from HBM by one or two
+// XCDs rather than by all eight.
 __device__ __forceinline__ bool decode_gemm_tile(const GemmArgs& a, int v, int& g, int& sp, int& tm, int& tn) {
   const int xcd = v & 7, local = v >> 3;
-  const int grp = xcd + 8 * (local / a.tiles_n);
+  const int ngroups = a.G * a.S * a.tiles_m;
+  const int gpx = (ngroups + 7) / 8;  // groups per XCD
+  const int lg = local / a.tiles_n;
+  const int grp = xcd * gpx + lg;
   tn = local % a.tiles_n;
-  if (grp >= a.G * a.S * a.tiles_m) return false;
+  if (lg >= gpx || grp >= ngroups) return false;
   tm = grp % a.tiles_m;
   sp = (grp / a.tiles_m) % a.S;
   g = grp / (a.tiles_m * a.S);
@@ -394,7 +403,7 @@ __device__ __forceinline__ void gemm_work(const GemmArgs& a, uint16_t* lds, int 
 
 template <bool AT, bool BT, bool SPLIT>
 __global__ __launch_bounds__(NT, 1) void butterfly_gemm(GemmArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint16_t lds[LDS_ELEMS];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds[RING_ELEMS];
   for (int v = blockIdx.x; v < a.vtiles; v += gridDim.x) {
     gemm_work<AT, BT, SPLIT>(a, lds, v);
     barrier();  // the staging area is read before the next tile's loads refill the ring
@@ -483,7 +492,7 @@ void set_geometry(GemmArgs& a, int M, int N, int K, int G, int S) {
     a.kchunk = cdiv(std::max(K, 1), BK) * BK;
     a.S = 1;
   }
-  a.vtiles = cdiv(int64_t(G) * a.S * a.tiles_m, 8) * 8 * a.tiles_n;
+  a.vtiles = 8 * cdiv(int64_t(G) * a.S * a.tiles_m, 8) * a.tiles_n;
 }
 
 // Splits of a weight-gradient product (K = tokens): enough work items for one
