@@ -118,6 +118,10 @@ def instrumented_step(opt, lr=0.02):
 def kernel_symbol(kind, gl, it, fp8=False):
     """The kernel (template instance) rocprof reports for a launch, as it
     appears in ``rocprofv3 --stats`` names (mmuon::(anonymous namespace)::...)."""
+    tp = "BF16T" if gl is not None and gl.struct.param_dtype == 1 else "F32T"
+    if gl is not None and kind in ("syrk", "poly", "px") and gl.struct.ns_dtype == 0:  # fp32 Newton-Schulz
+        stage = {"syrk": 0, "poly": 1}.get(kind, 2 if it < 4 else 3)
+        return f"ns_f32<{stage}, {tp if stage == 3 else 'F32T'}>"
     if kind == "syrk":
         return "ns_sym_bf16<0>"
     if kind == "poly":
@@ -125,7 +129,6 @@ def kernel_symbol(kind, gl, it, fp8=False):
     if kind == "px":
         if it < 4:
             return "ns_px_bf16<2, false, BF16T>"
-        tp = "BF16T" if gl.struct.param_dtype == 1 else "F32T"
         return f"ns_px_bf16<3, {'true' if gl.transposed else 'false'}, {tp}>"
     if kind == "pack":
         return ("fp8_" if fp8 else "") + ("pack_cols_kernel" if gl.transposed else "pack_rows_kernel")

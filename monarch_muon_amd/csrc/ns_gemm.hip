@@ -735,73 +735,113 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void ns_px_bf16(NsArgs a, int total)
 }
 
 // ---------------------------------------------------------------------------
-// fp32 Newton-Schulz (the pretrain copy keeps the buffer dtype).  Plain FMA
-// tiles: 64x64 outputs, 256 threads x (4x4), K tile 16.  All tiles computed.
+// fp32 Newton-Schulz (the pretrain copy keeps the buffer dtype) on the fp32
+// matrix cores (v_mfma_f32_32x32x2_f32, fp32 products and accumulation): 64x64
+// output tiles, 4 waves of 32x32, K tiles of 32 double-buffered in LDS (the
+// next tile's global loads are in flight during the current tile's MFMAs).
+// All tiles computed.
 // ---------------------------------------------------------------------------
 constexpr int FB = 64;
-constexpr int FK = 16;
+constexpr int FK = 32;
+constexpr int FPAD = FB + 32;  // LDS row: the two half-waves of a read hit disjoint banks
+
+// One K tile of the fp32 operands into registers: the row operand is 64 rows x
+// 32 k = 512 float4 (row idx/8, k chunk idx%8), two per thread; the column
+// operand the same from its own rows, or for PX 32 rows of X x 64 columns (row
+// idx/16, column chunk idx%16).
+struct F32Regs {
+  float4 a0, a1, b0, b1;
+};
+
+template <bool PX>
+__device__ __forceinline__ float4 f32_col_load(const float* rsrc, int64_t rld, const float* X, int64_t np_, int c0,
+                                               int k0, int idx) {
+  if (PX) return *reinterpret_cast<const float4*>(X + int64_t(k0 + (idx >> 4)) * np_ + c0 + 4 * (idx & 15));
+  return *reinterpret_cast<const float4*>(rsrc + int64_t(c0 + (idx >> 3)) * rld + k0 + 4 * (idx & 7));
+}
+
+template <bool PX>
+__device__ __forceinline__ void f32_load(F32Regs& g, const float* rsrc, int64_t rld, const float* X, int64_t np_,
+                                         int r0, int c0, int k0) {
+  const int i0 = threadIdx.x, i1 = threadIdx.x + 256;
+  g.a0 = *reinterpret_cast<const float4*>(rsrc + int64_t(r0 + (i0 >> 3)) * rld + k0 + 4 * (i0 & 7));
+  g.a1 = *reinterpret_cast<const float4*>(rsrc + int64_t(r0 + (i1 >> 3)) * rld + k0 + 4 * (i1 & 7));
+  g.b0 = f32_col_load<PX>(rsrc, rld, X, np_, c0, k0, i0);
+  g.b1 = f32_col_load<PX>(rsrc, rld, X, np_, c0, k0, i1);
+}
+
+template <int PAD>
+__device__ __forceinline__ void f32_store_t(const float4& v, float (*s)[PAD], int idx) {
+  const int r = idx >> 3, kc = 4 * (idx & 7);
+  s[kc][r] = v.x;
+  s[kc + 1][r] = v.y;
+  s[kc + 2][r] = v.z;
+  s[kc + 3][r] = v.w;
+}
+
+// The registers of f32_load into LDS buffers [k][row] / [k][col].
+template <bool PX, int PAD>
+__device__ __forceinline__ void f32_store(const F32Regs& g, float (*sa)[PAD], float (*sb)[PAD]) {
+  const int i0 = threadIdx.x, i1 = threadIdx.x + 256;
+  f32_store_t<PAD>(g.a0, sa, i0);
+  f32_store_t<PAD>(g.a1, sa, i1);
+  if (PX) {
+    *reinterpret_cast<float4*>(&sb[i0 >> 4][4 * (i0 & 15)]) = g.b0;
+    *reinterpret_cast<float4*>(&sb[i1 >> 4][4 * (i1 & 15)]) = g.b1;
+  } else {
+    f32_store_t<PAD>(g.b0, sb, i0);
+    f32_store_t<PAD>(g.b1, sb, i1);
+  }
+}
 
 template <int STAGE, class TP>
 __global__ __launch_bounds__(256) void ns_f32(NsArgs a) {
-  __shared__ float sa[FK][FB + 4];
-  __shared__ float sb[FK][FB + 4];
+  __shared__ float sa[2][FK][FPAD];  // row operand, [k][row]
+  __shared__ float sb[2][FK][FPAD];  // column operand, [k][col]
   const int b = blockIdx.z;
   const int ti = blockIdx.y, tj = blockIdx.x;
-  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
   const float* X = static_cast<const float*>(a.x_in) + int64_t(b) * a.mp * a.np;
   const float* A = static_cast<const float*>(a.a_in) + int64_t(b) * a.mp * a.mp;
-  int K;
-  if (STAGE == NS_SYRK) K = a.kx;
-  else K = a.mp;
-  float acc[4][4] = {};
-  for (int k0 = 0; k0 < K; k0 += FK) {
-    // thread loads one element of each operand tile: 64 rows x 16 k = 1024 = 4 per thread
+  constexpr bool PX = STAGE == NS_PX || STAGE == NS_PX_APPLY;
+  const int K = STAGE == NS_SYRK ? a.kx : a.mp;
+  // row operand: 64 rows x 32 k = 512 float4 (row idx/8, k chunk idx%8), two per thread;
+  // column operand: the same from X or A rows, or for PX 32 rows of X x 64 columns
+  // (row idx/16, column chunk idx%16)
+  const float* rsrc = STAGE == NS_SYRK ? X : A;
+  const int64_t rld = STAGE == NS_SYRK ? a.np : a.mp;
+  const int64_t np_ = a.np;
+  F32Regs g;
+  f32x16 acc = {};
+  const int KT = K / FK;
+  f32_load<PX>(g, rsrc, rld, X, np_, ti * FB, tj * FB, 0);
+  f32_store<PX, FPAD>(g, sa[0], sb[0]);
+  __syncthreads();
+  for (int t = 0; t < KT; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < KT) f32_load<PX>(g, rsrc, rld, X, np_, ti * FB, tj * FB, (t + 1) * FK);
+    // 32x32x2 steps: lane l supplies row (column) l%32 at k = 2 kk + l/32
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int idx = threadIdx.x + 256 * q;
-      const int r = idx >> 4, k = idx & 15;
-      float va, vb;
-      if (STAGE == NS_SYRK) {
-        va = X[int64_t(ti * FB + r) * a.np + k0 + k];
-        vb = X[int64_t(tj * FB + r) * a.np + k0 + k];
-      } else if (STAGE == NS_POLY) {
-        va = A[int64_t(ti * FB + r) * a.mp + k0 + k];
-        vb = A[int64_t(tj * FB + r) * a.mp + k0 + k];
-      } else {
-        va = A[int64_t(ti * FB + r) * a.mp + k0 + k];
-        // X[k][j] tile: 16 rows x 64 cols
-        const int kr = idx >> 6, c = idx & 63;
-        vb = X[int64_t(k0 + kr) * a.np + tj * FB + c];
-        sb[kr][c] = vb;
-      }
-      sa[k][r] = va;
-      if (STAGE != NS_PX && STAGE != NS_PX_APPLY) sb[k][r] = vb;
+    for (int kk = 0; kk < FK / 2; ++kk) {
+      const float av = sa[buf][2 * kk + (lane >> 5)][wr * 32 + (lane & 31)];
+      const float bv = sb[buf][2 * kk + (lane >> 5)][wc * 32 + (lane & 31)];
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
     }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < FK; ++k) {
-      float av[4], bv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        av[e] = sa[k][ty * 4 + e];
-        bv[e] = sb[k][tx * 4 + e];
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-#pragma unroll
-        for (int f = 0; f < 4; ++f) acc[e][f] = fmaf(av[e], bv[f], acc[e][f]);
-    }
+    if (t + 1 < KT) f32_store<PX, FPAD>(g, sa[buf ^ 1], sb[buf ^ 1]);
     __syncthreads();
   }
   const float s = a.scale != nullptr ? a.scale[b] : 1.f;
   typename TP::storage* prm = nullptr;
   if (STAGE == NS_PX_APPLY) prm = reinterpret_cast<typename TP::storage*>(a.blocks[b].param);
+  // accumulator value 4 q + e: column lane%32, row 8 q + 4 (lane/32) + e
+  const int j = tj * FB + wc * 32 + (lane & 31);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
+  for (int q = 0; q < 4; ++q) {
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      const int i = ti * FB + ty * 4 + e, j = tj * FB + tx * 4 + f;
-      float v = acc[e][f];
+    for (int e = 0; e < 4; ++e) {
+      const int i = ti * FB + wr * 32 + 8 * q + 4 * (lane >> 5) + e;
+      const float v = acc[4 * q + e];
       if (STAGE == NS_SYRK) {
         static_cast<float*>(a.out)[int64_t(b) * a.mp * a.mp + int64_t(i) * a.mp + j] = v * (s * s);
       } else if (STAGE == NS_POLY) {
@@ -819,8 +859,6 @@ __global__ __launch_bounds__(256) void ns_f32(NsArgs a) {
     }
   }
 }
-
-// Workgroups that fit on the device at once, a multiple of 8.
 
 template <int STAGE, class TP>
 void launch_bf16(const NsArgs& a, hipStream_t s) {
