@@ -387,7 +387,9 @@ def bench_butterfly(args, w):
         "frac_peak": round(total_fl / (wall_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "roofline": {"bound": "mfma", "kernel": "butterfly_gemm<false, false, false>", "achieved": round(achieved, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None, "avg_launch_ms": round(fwd_avg_launch, 4),
+                     "traffic": hbm_traffic("butterfly-6.89b" if tokens == 4096 and w.name == "6.89b-nb4" else "-",
+                                            "butterfly_gemm<false, false, false>"),
+                     "avg_launch_ms": round(fwd_avg_launch, 4),
                      "alg_flops_per_launch": fwd_fl / (2 * len(layer))},
         "forward_ms": round(fwd_ms, 4), "backward_ms": round(bwd_ms, 4),
         "torch_reference_ms": {"forward": round(ref_fwd_ms, 4), "backward": round(ref_bwd_ms, 4),
