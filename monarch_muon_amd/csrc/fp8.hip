@@ -213,14 +213,31 @@ __global__ __launch_bounds__(F8_NT) void fp8_pack_cols_kernel(PackArgs a, const 
 }
 
 // Zero the padding of an X stack (rows [m, mp), columns [n, np)): the FP8 pack
-// writes only the real region.
+// writes only the real region, and runs after this kernel.  Walks 8-column
+// chunks of the padding only: columns [n8, np) of every row (n8 = n rounded
+// down to 8; the real elements of a straddling chunk are rewritten by the pack),
+// then columns [0, n8) of rows [m, mp).  A chunk is 16 contiguous bytes in the
+// bf16 panel layout and 32 in the fp32 row-major one.
 template <class TX>
 __global__ __launch_bounds__(256) void zero_pads_kernel(void* xv, int m, int n, int mp, int np_) {
   auto* x = reinterpret_cast<typename TX::storage*>(xv) + int64_t(blockIdx.y) * mp * np_;
-  const int64_t total = int64_t(mp) * np_;
-  for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
-    const int i = int(e / np_), j = int(e % np_);
-    if (i >= m || j >= n) TX::store(x, TX::xoff(mp, np_, i, j), 0.f);
+  const int n8 = n & ~7;
+  const int cr = (np_ - n8) >> 3;                  // right-pad chunks per row
+  const int64_t right = int64_t(mp) * cr;
+  const int64_t total = right + int64_t(mp - m) * (n8 >> 3);
+  const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int64_t c = int64_t(blockIdx.x) * 256 + threadIdx.x; c < total; c += int64_t(gridDim.x) * 256) {
+    int i, j;
+    if (c < right) {
+      i = int(c / cr);
+      j = n8 + 8 * int(c - int64_t(i) * cr);
+    } else {
+      const int64_t d = c - right;
+      const int w = n8 >> 3;
+      i = m + int(d / w);
+      j = 8 * int(d - int64_t(i - m) * w);
+    }
+    Vec8<TX>::store(x + TX::xoff(mp, np_, i, j), z);
   }
 }
 
@@ -235,7 +252,7 @@ int launch_fp8_pack(const PackArgs& a, const mmuon_block_fp8* meta, int rows, in
                     hipStream_t s) {
   const dim3 grid(a.nparts, a.N), block(F8_NT);
   if (a.mp > a.m || a.np > a.n) {
-    const dim3 zg(64, a.N);
+    const dim3 zg(16, a.N);
     if (x_dtype == MMUON_BF16) hipLaunchKernelGGL((zero_pads_kernel<BF16T>), zg, dim3(256), 0, s, a.x, a.m, a.n, a.mp, a.np);
     else hipLaunchKernelGGL((zero_pads_kernel<F32T>), zg, dim3(256), 0, s, a.x, a.m, a.n, a.mp, a.np);
   }
