@@ -33,6 +33,8 @@ CASES = [
     (300, 4, 1024, 2752, 1024),   # 6.89B down
     (5000, 4, 256, 256, 256),     # split-K weight gradients, ragged last split
     (1, 4, 256, 256, 256),
+    (300, 1, 256, 512, 384),      # one block: the riffle is the identity
+    (200, 8, 256, 256, 264),      # eight blocks: 32-column planes, s not a multiple of 16
 ]
 
 
