@@ -70,9 +70,13 @@ constexpr bool col_t(int m) { return m != M_KK; }
 
 // MASK: the wave's 32x32 MFMA tiles (bit i*TMJ + j) that are computed; the
 // others, and the fragment reads only they need, are left out.
-template <int RK, int CK, int IDENT, int MASK = 0xFF>
+// SHARED: the row and column operands are the same rows (a diagonal tile of a
+// symmetric product): only the row-operand slice is loaded, and the column
+// fragments are read from it.
+template <int RK, int CK, int IDENT, int MASK = 0xFF, bool SHARED = false>
 struct Pipe {
   static_assert(RDMA == 2 && CDMA == 2, "two direct loads per thread and operand slice");
+  static constexpr int DMA = SHARED ? RDMA : SLICE_DMA;  // direct loads per thread and slice
   static constexpr bool tile_on(int i, int j) { return (MASK >> (i * TMJ + j)) & 1; }
   // fragment read G (column fragments first, then row fragments) feeds a computed tile
   static constexpr bool frag_on(int G) {
@@ -131,8 +135,10 @@ struct Pipe {
   __device__ __forceinline__ void issue(int src_kt, int slot_kt) const {
     issue_one<0>(src_kt, slot_kt);
     issue_one<1>(src_kt, slot_kt);
-    issue_one<2>(src_kt, slot_kt);
-    issue_one<3>(src_kt, slot_kt);
+    if constexpr (!SHARED) {
+      issue_one<2>(src_kt, slot_kt);
+      issue_one<3>(src_kt, slot_kt);
+    }
   }
 
   // Fragment read G (column fragments first, then row fragments) of k step KK
@@ -140,7 +146,7 @@ struct Pipe {
   template <int KK, int G, int M>
   __device__ __forceinline__ void load_one(int kt, Frags& f) const {
     const uint16_t* sr = rslot(kt);
-    const uint16_t* sc = sr + RSLICE;
+    const uint16_t* sc = SHARED ? sr : sr + RSLICE;
     if constexpr (G < TMJ)
       f.c[G] = col_t(M) ? frag_rowmajor_tr(sc, tfrag_c + G * 2048, KK) : frag_kmajor(sc, kfrag[KK], wn * WN + G * 32);
     else
@@ -172,7 +178,7 @@ struct Pipe {
     const int l16 = lane & 15, g = lane >> 4;
     const int k16 = 16 * (g & 1) + 4 * (l16 & 3);  // first column of the lane's 8-byte chunk
     if constexpr (IDENT == IDENT_ROW) {
-      const char* sc = reinterpret_cast<const char*>(rslot(kt) + RSLICE);
+      const char* sc = reinterpret_cast<const char*>(rslot(kt) + (SHARED ? 0 : RSLICE));
       const uint32_t base = uint32_t((4 * (g >> 1) + (l16 >> 2)) * 64 + k16 * 2);
 #pragma unroll
       for (int j = 0; j < TMJ; ++j)
@@ -221,7 +227,7 @@ struct Pipe {
     MMUON_STEP0(0) MMUON_STEP0(1) MMUON_STEP0(2) MMUON_STEP0(3)
     MMUON_STEP0(4) MMUON_STEP0(5) MMUON_STEP0(6) MMUON_STEP0(7)
 #undef MMUON_STEP0
-    wait_vm<(NSTAGE - 3) * SLICE_DMA>();  // slice kt+1; the later ones may stay in flight
+    wait_vm<(NSTAGE - 3) * DMA>();  // slice kt+1; the later ones may stay in flight
     barrier();
     // on the last step slice kt+1 does not exist and the reads of its slot go
     // unused; near the end a consumed slot is refilled with slice KT-1 so every
@@ -231,7 +237,7 @@ struct Pipe {
 #define MMUON_STEP1(g)                                                               \
     MMUON_MFMA(fb, g)                                                                \
     if constexpr ((g) < TMI + TMJ && frag_on(g)) load_one<0, (g), MN>(kt + 1, fa);   \
-    if constexpr ((g) < SLICE_DMA) issue_one<(g)>(src, slot);                        \
+    if constexpr ((g) < DMA) issue_one<(g)>(src, slot);                              \
     __builtin_amdgcn_sched_barrier(0);
     MMUON_STEP1(0) MMUON_STEP1(1) MMUON_STEP1(2) MMUON_STEP1(3)
     MMUON_STEP1(4) MMUON_STEP1(5) MMUON_STEP1(6) MMUON_STEP1(7)
@@ -257,10 +263,10 @@ struct Pipe {
       for (int j = 0; j < TMJ; ++j) acc[i][j] = f32x16{};
 #pragma unroll
     for (int q = 0; q < NSTAGE - 1; ++q) issue(q < KT ? q : KT - 1, q);
-    wait_vm<(NSTAGE - 2) * SLICE_DMA>();
+    wait_vm<(NSTAGE - 2) * DMA>();
     barrier();
     for (int kt = 0; kt < KT; ++kt) {
-      wait_vm<(NSTAGE - 3) * SLICE_DMA>();
+      wait_vm<(NSTAGE - 3) * DMA>();
       barrier();
       const int src = kt + NSTAGE - 1 < KT ? kt + NSTAGE - 1 : KT - 1;
       issue(src, kt + NSTAGE - 1);
@@ -279,7 +285,7 @@ struct Pipe {
     // slices 0 .. NSTAGE-2 (beyond the last slice: refills with slice KT-1)
 #pragma unroll
     for (int q = 0; q < NSTAGE - 1; ++q) issue(q < KT ? q : KT - 1, q);
-    wait_vm<(NSTAGE - 2) * SLICE_DMA>();  // slice 0 visible, the others may stay in flight
+    wait_vm<(NSTAGE - 2) * DMA>();  // slice 0 visible, the others may stay in flight
     barrier();
     Frags fa, fb;
     if (t1 > 0) load<0, M_TT>(0, fa);
@@ -346,12 +352,12 @@ __device__ __forceinline__ int diag_wave_role(int wave) {
   return below_diag(wm, wn) ? WAVE_IDLE : (on_diag(wm, wn) ? WAVE_DIAG : WAVE_FULL);
 }
 
-template <int RK, int CK, int IDENT, int MASK>
+template <int RK, int CK, int IDENT, int MASK, bool SHARED>
 __device__ __forceinline__ void mainloop_run(const uint16_t* rsrc_k, const uint16_t* rsrc_t, int thr_r,
                                              const uint16_t* csrc_k, const uint16_t* csrc_t, int thr_c,
                                              int64_t pstride, int KT, uint16_t* lds, f32x16 (&acc)[TMI][TMJ],
                                              float ident_v, int diag, bool loads_only) {
-  Pipe<RK, CK, IDENT, MASK> p;
+  Pipe<RK, CK, IDENT, MASK, SHARED> p;
   p.rsrc_k = rsrc_k;
   p.rsrc_t = rsrc_t;
   p.csrc_k = csrc_k;
@@ -380,19 +386,25 @@ __device__ __forceinline__ void mainloop_run(const uint16_t* rsrc_k, const uint1
 // Operand sources: *_k the K form (panel 0 at the operand's first row), *_t the
 // T form (row 0 of the first panel holding the operand's rows); thr_*: slices
 // kt < thr are T (OP_SPLIT); pstride: elements per panel.  ident_v: the identity
-// scalar; diag: K index of the tile's first row (IDENT_ROW) or column (IDENT_COL);
-// role (wave-uniform): WAVE_FULL, or this wave's role in a diagonal tile.
+// scalar; diag: K index of the tile's first row (IDENT_ROW) or column (IDENT_COL).
+// sym_diag (workgroup-uniform): a diagonal tile of a symmetric product, whose
+// row and column operands are the same rows (loaded once, Pipe SHARED); role
+// (wave-uniform) is then this wave's role in it.
 template <int RK, int CK, int IDENT = IDENT_NONE>
 __device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t* rsrc_t, int thr_r,
                                          const uint16_t* csrc_k, const uint16_t* csrc_t, int thr_c,
                                          int64_t pstride, int KT, uint16_t* lds, f32x16 (&acc)[TMI][TMJ],
-                                         float ident_v = 0.f, int diag = 0, int role = WAVE_FULL) {
-  if (role == WAVE_DIAG)
-    mainloop_run<RK, CK, IDENT, MASK_DIAG>(rsrc_k, rsrc_t, thr_r, csrc_k, csrc_t, thr_c, pstride, KT, lds, acc,
-                                           ident_v, diag, false);
+                                         float ident_v = 0.f, int diag = 0, bool sym_diag = false,
+                                         int role = WAVE_FULL) {
+  if (!sym_diag)
+    mainloop_run<RK, CK, IDENT, 0xFF, false>(rsrc_k, rsrc_t, thr_r, csrc_k, csrc_t, thr_c, pstride, KT, lds, acc,
+                                             ident_v, diag, false);
+  else if (role == WAVE_DIAG)
+    mainloop_run<RK, CK, IDENT, MASK_DIAG, true>(rsrc_k, rsrc_t, thr_r, csrc_k, csrc_t, thr_c, pstride, KT, lds,
+                                                 acc, ident_v, diag, false);
   else
-    mainloop_run<RK, CK, IDENT, 0xFF>(rsrc_k, rsrc_t, thr_r, csrc_k, csrc_t, thr_c, pstride, KT, lds, acc,
-                                      ident_v, diag, role == WAVE_IDLE);
+    mainloop_run<RK, CK, IDENT, 0xFF, true>(rsrc_k, rsrc_t, thr_r, csrc_k, csrc_t, thr_c, pstride, KT, lds, acc,
+                                            ident_v, diag, role == WAVE_IDLE);
 }
 
 // D[i][j] accumulators of this wave -> T[j][i] in the staging area, each value
@@ -514,11 +526,11 @@ __device__ __forceinline__ void sym_work(const NsArgs& a, uint16_t* lds, int v) 
   f32x16 acc[TMI][TMJ];
   if (STAGE == NS_SYRK)
     mainloop<OP_K, OP_K>(src + r0 * PANEL, nullptr, 0, src + c0 * PANEL, nullptr, 0, pstride, K / BK, lds, acc,
-                         0.f, 0, role);
+                         0.f, 0, diag, role);
   else  // acc = A A + (b/c) A, so P = c acc = b A + c A A
     mainloop<OP_SPLIT, OP_SPLIT, IDENT_COL>(src + r0 * PANEL, src + (r0 / PANEL) * pstride, r0 / BK,
                                             src + c0 * PANEL, src + (c0 / PANEL) * pstride, c0 / BK,
-                                            pstride, K / BK, lds, acc, a.cb / a.cc, c0, role);
+                                            pstride, K / BK, lds, acc, a.cb / a.cc, c0, diag, role);
 
   float f = STAGE == NS_POLY ? a.cc : 1.f;  // SYRK: s^2 on the first iteration
   if (STAGE == NS_SYRK && a.scale != nullptr) {
