@@ -254,26 +254,6 @@ struct Pipe {
     body<M, MN, -1>(b - 1, fa, fb, acc);
   }
 
-  // The direct loads and barriers of run() without the matrix work: a wave
-  // whose sub-tile is not needed keeps the workgroup's ring filled.
-  __device__ __forceinline__ void run_loads_only(f32x16 (&acc)[TMI][TMJ]) const {
-#pragma unroll
-    for (int i = 0; i < TMI; ++i)
-#pragma unroll
-      for (int j = 0; j < TMJ; ++j) acc[i][j] = f32x16{};
-#pragma unroll
-    for (int q = 0; q < NSTAGE - 1; ++q) issue(q < KT ? q : KT - 1, q);
-    wait_vm<(NSTAGE - 2) * DMA>();
-    barrier();
-    for (int kt = 0; kt < KT; ++kt) {
-      wait_vm<(NSTAGE - 3) * DMA>();
-      barrier();
-      const int src = kt + NSTAGE - 1 < KT ? kt + NSTAGE - 1 : KT - 1;
-      issue(src, kt + NSTAGE - 1);
-    }
-    wait_vm<0>();
-  }
-
   __device__ __forceinline__ void run(f32x16 (&acc)[TMI][TMJ]) const {
 #pragma unroll
     for (int i = 0; i < TMI; ++i)
@@ -323,40 +303,55 @@ struct Pipe {
   }
 };
 
-// Roles of the waves in a diagonal tile of a symmetric product.  A 128 x 64
-// sub-tile strictly below the tile's diagonal is the transpose of one above it
-// (its wave only issues its direct loads); a sub-tile that starts on the
-// diagonal computes only its 32 x 32 tiles on or above it (MASK_DIAG).
-enum { WAVE_FULL = 0, WAVE_DIAG = 1, WAVE_IDLE = 2 };
-__device__ __forceinline__ bool below_diag(int wm, int wn) { return (wn + 1) * WN <= wm * WM; }
-__device__ __forceinline__ bool on_diag(int wm, int wn) { return wn * WN == wm * WM; }
-constexpr int mask_diag() {
+// Wave plan of a diagonal tile of a symmetric product.  Only its 36 32 x 32
+// MFMA tiles on or above the diagonal (R <= C, units of 32 rows / columns) are
+// computed; they are dealt to the 8 waves so that the two waves of every SIMD
+// (waves w and w + 4) hold 9 between them, against 16 per SIMD in a full tile.
+// Wave w computes, inside the 128 x 64 window (vwm, vwn) of the regular wave
+// grid (rows 128 vwm.., columns 64 vwn..), the 32 x 32 tiles of its mask
+// (bit i * TMJ + j: window tile row i, column j):
+//   w0 (0,2) all 8      w4 (0,1) tile (3,1) = (R 3, C 3)
+//   w1 (0,3) all 8      w5 (1,3) tile (3,1) = (R 7, C 7)
+//   w2 (0,0) j >= i: 3  w6 (0,1) rows 0-2: 6
+//   w3 (1,2) j >= i: 3  w7 (1,3) rows 0-2: 6
+// Every tile on or above the diagonal is computed by exactly one wave and no
+// tile below it by any; the staging fills those from their transposes.
+constexpr int mask_upper() {
   int m = 0;
   for (int i = 0; i < TMI; ++i)
     for (int j = 0; j < TMJ; ++j)
       if (j >= i) m |= 1 << (i * TMJ + j);
   return m;
 }
-constexpr int MASK_DIAG = mask_diag();
-static_assert(WM == 2 * WN && BM == 2 * WM, "sub-tiles below the diagonal mirror sub-tiles above it");
+constexpr int MASK_FULL = 0xFF;
+constexpr int MASK_UPPER = mask_upper();        // (0,0), (0,1), (1,1)
+constexpr int MASK_LAST = 1 << (3 * TMJ + 1);   // (3,1)
+constexpr int MASK_FIRST6 = (1 << (3 * TMJ)) - 1;  // rows 0-2
+static_assert(TMI == 4 && TMJ == 2 && BM == 8 * 32 && WM == 4 * 32 && WN == 2 * 32,
+              "the plan deals the 8 x 8 grid of 32 x 32 tiles of a 256 x 256 tile");
 
-// 32 x 32 tile (R, C) of a diagonal tile (units of 32 rows / columns) is
-// computed by the wave that owns it.
-__device__ __forceinline__ bool diag_tile_computed(int R, int C) {
-  const int wm = R / (WM / 32), wn = C / (WN / 32);
-  if (below_diag(wm, wn)) return false;
-  return !on_diag(wm, wn) || C >= R;
+struct WavePlan {
+  int vwm, vwn, mask;
+};
+__device__ __forceinline__ WavePlan diag_plan(int wave) {
+  switch (wave) {
+    case 0: return {0, 2, MASK_FULL};
+    case 1: return {0, 3, MASK_FULL};
+    case 2: return {0, 0, MASK_UPPER};
+    case 3: return {1, 2, MASK_UPPER};
+    case 4: return {0, 1, MASK_LAST};
+    case 5: return {1, 3, MASK_LAST};
+    case 6: return {0, 1, MASK_FIRST6};
+    default: return {1, 3, MASK_FIRST6};
+  }
 }
-__device__ __forceinline__ int diag_wave_role(int wave) {
-  const int wm = wave / NWN, wn = wave % NWN;
-  return below_diag(wm, wn) ? WAVE_IDLE : (on_diag(wm, wn) ? WAVE_DIAG : WAVE_FULL);
-}
+__device__ __forceinline__ WavePlan full_plan(int wave) { return {wave / NWN, wave % NWN, MASK_FULL}; }
 
 template <int RK, int CK, int IDENT, int MASK, bool SHARED>
 __device__ __forceinline__ void mainloop_run(const uint16_t* rsrc_k, const uint16_t* rsrc_t, int thr_r,
                                              const uint16_t* csrc_k, const uint16_t* csrc_t, int thr_c,
                                              int64_t pstride, int KT, uint16_t* lds, f32x16 (&acc)[TMI][TMJ],
-                                             float ident_v, int diag, bool loads_only) {
+                                             float ident_v, int diag, int vwm, int vwn) {
   Pipe<RK, CK, IDENT, MASK, SHARED> p;
   p.rsrc_k = rsrc_k;
   p.rsrc_t = rsrc_t;
@@ -367,9 +362,9 @@ __device__ __forceinline__ void mainloop_run(const uint16_t* rsrc_k, const uint1
   p.pstride = pstride;
   p.KT = KT;
   p.lane = threadIdx.x & 63;
-  p.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  p.wm = p.wave / NWN;
-  p.wn = p.wave % NWN;
+  p.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // its share of the direct loads
+  p.wm = vwm;                                                 // its window of the output tile
+  p.wn = vwn;
   p.lds = lds;
   p.lds0 = lds_addr(lds);
   p.k_loff = kmajor_lane_offset(p.lane);
@@ -379,8 +374,7 @@ __device__ __forceinline__ void mainloop_run(const uint16_t* rsrc_k, const uint1
   p.tfrag_c = rowmajor_frag_base(p.wn * TMJ, p.lane);
   p.diag0 = diag + (IDENT == IDENT_ROW ? p.wm * WM : p.wn * WN);
   p.id_v = ident_v;
-  if (loads_only) p.run_loads_only(acc);
-  else p.run(acc);
+  p.run(acc);
 }
 
 // Operand sources: *_k the K form (panel 0 at the operand's first row), *_t the
@@ -388,41 +382,44 @@ __device__ __forceinline__ void mainloop_run(const uint16_t* rsrc_k, const uint1
 // kt < thr are T (OP_SPLIT); pstride: elements per panel.  ident_v: the identity
 // scalar; diag: K index of the tile's first row (IDENT_ROW) or column (IDENT_COL).
 // sym_diag (workgroup-uniform): a diagonal tile of a symmetric product, whose
-// row and column operands are the same rows (loaded once, Pipe SHARED); role
-// (wave-uniform) is then this wave's role in it.
+// row and column operands are the same rows (loaded once, Pipe SHARED) and
+// whose work is dealt by diag_plan.
 template <int RK, int CK, int IDENT = IDENT_NONE>
 __device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t* rsrc_t, int thr_r,
                                          const uint16_t* csrc_k, const uint16_t* csrc_t, int thr_c,
                                          int64_t pstride, int KT, uint16_t* lds, f32x16 (&acc)[TMI][TMJ],
-                                         float ident_v = 0.f, int diag = 0, bool sym_diag = false,
-                                         int role = WAVE_FULL) {
-  if (!sym_diag)
-    mainloop_run<RK, CK, IDENT, 0xFF, false>(rsrc_k, rsrc_t, thr_r, csrc_k, csrc_t, thr_c, pstride, KT, lds, acc,
-                                             ident_v, diag, false);
-  else if (role == WAVE_DIAG)
-    mainloop_run<RK, CK, IDENT, MASK_DIAG, true>(rsrc_k, rsrc_t, thr_r, csrc_k, csrc_t, thr_c, pstride, KT, lds,
-                                                 acc, ident_v, diag, false);
-  else
-    mainloop_run<RK, CK, IDENT, 0xFF, true>(rsrc_k, rsrc_t, thr_r, csrc_k, csrc_t, thr_c, pstride, KT, lds, acc,
-                                            ident_v, diag, role == WAVE_IDLE);
+                                         float ident_v = 0.f, int diag = 0, bool sym_diag = false) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const WavePlan plan = sym_diag ? diag_plan(wave) : full_plan(wave);
+#define MMUON_RUN(MASK, SH)                                                                                  \
+  mainloop_run<RK, CK, IDENT, MASK, SH>(rsrc_k, rsrc_t, thr_r, csrc_k, csrc_t, thr_c, pstride, KT, lds, acc, \
+                                        ident_v, diag, plan.vwm, plan.vwn)
+  if (!sym_diag) MMUON_RUN(MASK_FULL, false);
+  else if (plan.mask == MASK_FULL) MMUON_RUN(MASK_FULL, true);
+  else if (plan.mask == MASK_UPPER) MMUON_RUN(MASK_UPPER, true);
+  else if (plan.mask == MASK_LAST) MMUON_RUN(MASK_LAST, true);
+  else MMUON_RUN(MASK_FIRST6, true);
+#undef MMUON_RUN
 }
 
 // D[i][j] accumulators of this wave -> T[j][i] in the staging area, each value
 // scaled by f before the bf16 rounding.  Lane geometry: the lane holds column
-// j = 64 wn + 32 tj + lane%32 and rows i = 128 wm + 32 ti + 8 qg + 4 (lane/32) + e.
-// diag: a diagonal tile of a symmetric product; its 32 x 32 tiles that were not
-// computed are filled from their transposes, T[i][j] = D[i][j].
+// j = 64 wn + 32 tj + lane%32 and rows i = 128 wm + 32 ti + 8 qg + 4 (lane/32) + e,
+// (wm, wn) the wave's window.  diag: a diagonal tile of a symmetric product
+// computed by diag_plan; every computed tile above the diagonal also fills its
+// mirror below it, T[i][j] = D[i][j].
 __device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI][TMJ], float f,
                                            bool diag = false) {
   const int tid = fresh_tid();
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / NWN, wn = wave % NWN;
+  const WavePlan plan = diag ? diag_plan(wave) : full_plan(wave);
+  const int wm = plan.vwm, wn = plan.vwn;
 #pragma unroll
   for (int i = 0; i < TMI; ++i) {
 #pragma unroll
     for (int j = 0; j < TMJ; ++j) {
       const int R = wm * (WM / 32) + i, C = wn * (WN / 32) + j;
-      if (diag && !diag_tile_computed(R, C)) continue;
+      if (!((plan.mask >> (i * TMJ + j)) & 1)) continue;
 #pragma unroll
       for (int qg = 0; qg < 4; ++qg) {
         float v[4];
@@ -432,7 +429,7 @@ __device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI]
         const int col = wm * WM + i * 32 + qg * 8 + (lane >> 5) * 4;
         *reinterpret_cast<uint2*>(stage + tile_off(row, col)) = make_uint2(f2bf2(v[0], v[1]), f2bf2(v[2], v[3]));
       }
-      if (diag && C > R && !diag_tile_computed(C, R)) {
+      if (diag && C > R) {
 #pragma unroll
         for (int qg = 0; qg < 4; ++qg)
 #pragma unroll
@@ -522,15 +519,14 @@ __device__ __forceinline__ void sym_work(const NsArgs& a, uint16_t* lds, int v) 
   // on a diagonal tile only the 32 x 32 tiles on or above the diagonal are
   // computed; the others are staged from their transposes
   const bool diag = tc == ti;
-  const int role = diag ? diag_wave_role(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) : WAVE_FULL;
   f32x16 acc[TMI][TMJ];
   if (STAGE == NS_SYRK)
     mainloop<OP_K, OP_K>(src + r0 * PANEL, nullptr, 0, src + c0 * PANEL, nullptr, 0, pstride, K / BK, lds, acc,
-                         0.f, 0, diag, role);
+                         0.f, 0, diag);
   else  // acc = A A + (b/c) A, so P = c acc = b A + c A A
     mainloop<OP_SPLIT, OP_SPLIT, IDENT_COL>(src + r0 * PANEL, src + (r0 / PANEL) * pstride, r0 / BK,
                                             src + c0 * PANEL, src + (c0 / PANEL) * pstride, c0 / BK,
-                                            pstride, K / BK, lds, acc, a.cb / a.cc, c0, diag, role);
+                                            pstride, K / BK, lds, acc, a.cb / a.cc, c0, diag);
 
   float f = STAGE == NS_POLY ? a.cc : 1.f;  // SYRK: s^2 on the first iteration
   if (STAGE == NS_SYRK && a.scale != nullptr) {
