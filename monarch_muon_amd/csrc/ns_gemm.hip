@@ -383,18 +383,22 @@ __device__ __forceinline__ void mainloop_run(const uint16_t* rsrc_k, const uint1
 // scalar; diag: K index of the tile's first row (IDENT_ROW) or column (IDENT_COL).
 // sym_diag (workgroup-uniform): a diagonal tile of a symmetric product, whose
 // row and column operands are the same rows (loaded once, Pipe SHARED) and
-// whose work is dealt by diag_plan.
+// whose work is dealt by diag_plan.  idle (wave-uniform, full tiles only): the
+// wave's window holds only zero padding columns; it issues its share of the
+// direct loads and leaves its accumulators zero.
 template <int RK, int CK, int IDENT = IDENT_NONE>
 __device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t* rsrc_t, int thr_r,
                                          const uint16_t* csrc_k, const uint16_t* csrc_t, int thr_c,
                                          int64_t pstride, int KT, uint16_t* lds, f32x16 (&acc)[TMI][TMJ],
-                                         float ident_v = 0.f, int diag = 0, bool sym_diag = false) {
+                                         float ident_v = 0.f, int diag = 0, bool sym_diag = false,
+                                         bool idle = false) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const WavePlan plan = sym_diag ? diag_plan(wave) : full_plan(wave);
 #define MMUON_RUN(MASK, SH)                                                                                  \
   mainloop_run<RK, CK, IDENT, MASK, SH>(rsrc_k, rsrc_t, thr_r, csrc_k, csrc_t, thr_c, pstride, KT, lds, acc, \
                                         ident_v, diag, plan.vwm, plan.vwn)
-  if (!sym_diag) MMUON_RUN(MASK_FULL, false);
+  if (!sym_diag && idle) MMUON_RUN(0, false);
+  else if (!sym_diag) MMUON_RUN(MASK_FULL, false);
   else if (plan.mask == MASK_FULL) MMUON_RUN(MASK_FULL, true);
   else if (plan.mask == MASK_UPPER) MMUON_RUN(MASK_UPPER, true);
   else if (plan.mask == MASK_LAST) MMUON_RUN(MASK_LAST, true);
@@ -617,9 +621,12 @@ __device__ __forceinline__ void px_work(const NsArgs& a, uint16_t* lds, int v) {
   const uint16_t* P = static_cast<const uint16_t*>(a.a_in) + int64_t(b) * a.mp * a.mp;
   const uint16_t* X = static_cast<const uint16_t*>(a.x_in) + int64_t(b) * a.mp * a.np + (c0 / PANEL) * pstride;
   f32x16 acc[TMI][TMJ];
-  // acc = P X + a X (the a X term added from the X slices of the tile's diagonal rows)
+  // acc = P X + a X (the a X term added from the X slices of the tile's diagonal
+  // rows); a wave whose 64 columns all lie in the zero padding (n <= column <
+  // np) computes nothing: its part of X' stays zero
+  const int wn = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) % NWN;
   mainloop<OP_SPLIT, OP_T, IDENT_ROW>(P + r0 * PANEL, P + (r0 / PANEL) * pstride, r0 / BK, nullptr, X, 0,
-                                      pstride, a.mp / BK, lds, acc, a.ca, r0);
+                                      pstride, a.mp / BK, lds, acc, a.ca, r0, false, c0 + wn * WN >= a.n);
 
   const float s = a.scale != nullptr ? a.scale[b] : 1.f;
   char* stage = reinterpret_cast<char*>(lds);
