@@ -42,7 +42,8 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_kernel(AdamWArgs a) {
   auto* v = reinterpret_cast<typename TS::storage*>(T.exp_avg_sq);
   int64_t tail = start;
   // 8 elements per thread and 16-B accesses when all four streams are aligned
-  // here; two groups' loads are issued before either is computed
+  // here; two groups' loads are issued before either is computed; every access
+  // is non-temporal (each element is read and written once per step)
   const uintptr_t al = reinterpret_cast<uintptr_t>(p + start) | reinterpret_cast<uintptr_t>(g + start) |
                        reinterpret_cast<uintptr_t>(m + start) | reinterpret_cast<uintptr_t>(v + start);
   if ((al & 15) == 0) {
@@ -51,15 +52,15 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_kernel(AdamWArgs a) {
       const int64_t i1 = i0 + ADAM_NT * 8;
       const bool two = i1 < stop;
       float P[2][8], G[2][8], M[2][8], V[2][8];
-      Vec8<TP>::load(p + i0, P[0]);
-      Vec8<TG>::load(g + i0, G[0]);
-      Vec8<TS>::load(m + i0, M[0]);
-      Vec8<TS>::load(v + i0, V[0]);
+      Vec8<TP>::load_nt(p + i0, P[0]);
+      Vec8<TG>::load_nt(g + i0, G[0]);
+      Vec8<TS>::load_nt(m + i0, M[0]);
+      Vec8<TS>::load_nt(v + i0, V[0]);
       if (two) {
-        Vec8<TP>::load(p + i1, P[1]);
-        Vec8<TG>::load(g + i1, G[1]);
-        Vec8<TS>::load(m + i1, M[1]);
-        Vec8<TS>::load(v + i1, V[1]);
+        Vec8<TP>::load_nt(p + i1, P[1]);
+        Vec8<TG>::load_nt(g + i1, G[1]);
+        Vec8<TS>::load_nt(m + i1, M[1]);
+        Vec8<TS>::load_nt(v + i1, V[1]);
       }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -67,9 +68,9 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_kernel(AdamWArgs a) {
         const int64_t i = h ? i1 : i0;
 #pragma unroll
         for (int e = 0; e < 8; ++e) adamw_elem<TP, TS>(P[h][e], clipped<TG>(G[h][e], a.gscale), M[h][e], V[h][e], a);
-        Vec8<TP>::store(p + i, P[h]);
-        Vec8<TS>::store(m + i, M[h]);
-        Vec8<TS>::store(v + i, V[h]);
+        Vec8<TP>::store_nt(p + i, P[h]);
+        Vec8<TS>::store_nt(m + i, M[h]);
+        Vec8<TS>::store_nt(v + i, V[h]);
       }
     }
     tail = stop;

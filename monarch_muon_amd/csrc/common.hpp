@@ -65,13 +65,23 @@ struct BF16T {
   }
 };
 
-// 8 consecutive elements, vector access (16-B aligned)
+// 16-B non-temporal (streaming) access: data read or written once per pass
+typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load16_nt(const void* p) {
+  const u32x4_nt r = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(p));
+  return make_uint4(r.x, r.y, r.z, r.w);
+}
+__device__ __forceinline__ void store16_nt(void* p, const uint4& v) {
+  const u32x4_nt r = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(r, reinterpret_cast<u32x4_nt*>(p));
+}
+
+// 8 consecutive elements, vector access (16-B aligned); *_nt: non-temporal
 template <class T>
 struct Vec8;
 template <>
 struct Vec8<BF16T> {
-  static __device__ __forceinline__ void load(const uint16_t* p, float v[8]) {
-    const uint4 r = *reinterpret_cast<const uint4*>(p);
+  static __device__ __forceinline__ void unpack(const uint4& r, float v[8]) {
     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -79,14 +89,22 @@ struct Vec8<BF16T> {
       v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
     }
   }
-  static __device__ __forceinline__ void store(uint16_t* p, const float v[8]) {
+  static __device__ __forceinline__ uint4 pack(const float v[8]) {
     uint4 r;
     r.x = uint32_t(f2bf(v[0])) | (uint32_t(f2bf(v[1])) << 16);
     r.y = uint32_t(f2bf(v[2])) | (uint32_t(f2bf(v[3])) << 16);
     r.z = uint32_t(f2bf(v[4])) | (uint32_t(f2bf(v[5])) << 16);
     r.w = uint32_t(f2bf(v[6])) | (uint32_t(f2bf(v[7])) << 16);
-    *reinterpret_cast<uint4*>(p) = r;
+    return r;
   }
+  static __device__ __forceinline__ void load(const uint16_t* p, float v[8]) {
+    unpack(*reinterpret_cast<const uint4*>(p), v);
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, const float v[8]) {
+    *reinterpret_cast<uint4*>(p) = pack(v);
+  }
+  static __device__ __forceinline__ void load_nt(const uint16_t* p, float v[8]) { unpack(load16_nt(p), v); }
+  static __device__ __forceinline__ void store_nt(uint16_t* p, const float v[8]) { store16_nt(p, pack(v)); }
 };
 template <>
 struct Vec8<F32T> {
@@ -99,6 +117,15 @@ struct Vec8<F32T> {
   static __device__ __forceinline__ void store(float* p, const float v[8]) {
     reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
     reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+  static __device__ __forceinline__ void load_nt(const float* p, float v[8]) {
+    const uint4 a = load16_nt(p), b = load16_nt(p + 4);
+    v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y); v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
+    v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y); v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
+  }
+  static __device__ __forceinline__ void store_nt(float* p, const float v[8]) {
+    store16_nt(p, make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])));
+    store16_nt(p + 4, make_uint4(__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]), __float_as_uint(v[7])));
   }
 };
 

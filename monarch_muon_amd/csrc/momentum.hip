@@ -64,8 +64,9 @@ __global__ __launch_bounds__(PACK_NT) void pack_rows_kernel(PackArgs a) {
           v[q] = TX::round(bv[it][q]);
           ss += v[q] * v[q];
         }
-        Vec8<TB>::store(buf + s0 + it * 64, bv[it]);
-        Vec8<TX>::store(x + TX::xoff(a.mp, a.np, i, j0 + it * 64), v);
+        // streaming stores (each line written once by this pass)
+        Vec8<TB>::store_nt(buf + s0 + it * 64, bv[it]);
+        Vec8<TX>::store_nt(x + TX::xoff(a.mp, a.np, i, j0 + it * 64), v);
       }
       const float tot = block_sum<PACK_NT>(ss, red);
       if (threadIdx.x == 0) a.partial[int64_t(b) * a.nparts + blockIdx.x] = tot;
