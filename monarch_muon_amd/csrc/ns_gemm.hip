@@ -120,11 +120,15 @@ struct Pipe {
   // covers operand rows 16 (2w + q) .. +15 of the panel (1 KiB); T form: panel
   // w of the operand, k rows 16q .. 16q+15 of the slice (1 KiB).  Either way the
   // load lands at byte (2w + q) * 1024 of the operand's slice.
-  template <int Q>
+  // RF >= 0: the slice pair is in form RF (known when the slice lies in the same
+  // run as the step that loads it); RF < 0: decided from the slice index.
+  template <int Q, int RF = -1>
   __device__ __forceinline__ void issue_one(int src_kt, int slot_kt) const {
     constexpr int q = Q & 1;
     const uint32_t dst = lds0 + (slot_kt % NSTAGE) * SLOT * 2 + (Q < 2 ? 0 : RSLICE * 2) + (2 * wave + q) * 1024;
-    const bool t = Q < 2 ? row_is_t(src_kt) : col_is_t(src_kt);
+    bool t;
+    if constexpr (RF >= 0) t = Q < 2 ? row_t(RF) : col_t(RF);
+    else t = Q < 2 ? row_is_t(src_kt) : col_is_t(src_kt);
     const uint16_t* srck = Q < 2 ? rsrc_k : csrc_k;
     const uint16_t* srct = Q < 2 ? rsrc_t : csrc_t;
     if (t)
@@ -207,14 +211,15 @@ struct Pipe {
   }
 
   // Step kt: slice kt is consumed in form M, slice kt+1 (its k step 0 fragments)
-  // is read in form MN.  Fragments ping-pong at half-slice granularity: the k
+  // is read in form MN, and slice kt+NSTAGE-1 is loaded in form RF (RF < 0:
+  // decided from its index).  Fragments ping-pong at half-slice granularity: the k
   // step 1 reads of slice kt go out one per MFMA of its k step 0, and (after
   // the slice-kt+1 barrier) the k step 0 reads of slice kt+1 one per MFMA of
   // the k step 1.  At the barrier of step kt every wave has consumed slice
   // kt-1, so its slot takes slice kt+NSTAGE-1; those direct loads are
   // interleaved one by one with the k step 1 MFMAs as well.  F >= 0: the
   // slice crosses this wave's identity at tile F (ident_add).
-  template <int M, int MN, int F>
+  template <int M, int MN, int F, int RF = -1>
   __device__ __forceinline__ void body(int kt, Frags& fa, Frags& fb, f32x16 (&acc)[TMI][TMJ]) const {
     static_assert(TMI * TMJ == 8 && SLICE_DMA <= 8 && TMI + TMJ <= 8, "one read / direct load per MFMA");
 #define MMUON_MFMA(f, g)                                                                          \
@@ -237,7 +242,7 @@ struct Pipe {
 #define MMUON_STEP1(g)                                                               \
     MMUON_MFMA(fb, g)                                                                \
     if constexpr ((g) < TMI + TMJ && frag_on(g)) load_one<0, (g), MN>(kt + 1, fa);   \
-    if constexpr ((g) < DMA) issue_one<(g)>(src, slot);                              \
+    if constexpr ((g) < DMA) issue_one<(g), RF>(src, slot);                          \
     __builtin_amdgcn_sched_barrier(0);
     MMUON_STEP1(0) MMUON_STEP1(1) MMUON_STEP1(2) MMUON_STEP1(3)
     MMUON_STEP1(4) MMUON_STEP1(5) MMUON_STEP1(6) MMUON_STEP1(7)
@@ -247,10 +252,13 @@ struct Pipe {
     if constexpr (F >= 0) ident_add<F>(kt, acc);
   }
 
-  // Slices a .. b-1 in form M (b > a), the last of them reading slice b in form MN.
+  // Slices a .. b-1 in form M (b > a), the last of them reading slice b in form
+  // MN.  The steps that load a slice of the same run know its form.
   template <int M, int MN>
   __device__ __forceinline__ void run_span(int a, int b, Frags& fa, Frags& fb, f32x16 (&acc)[TMI][TMJ]) const {
-    for (int kt = a; kt < b - 1; ++kt) body<M, M, -1>(kt, fa, fb, acc);
+    int kt = a;
+    for (; kt < b - (NSTAGE - 1); ++kt) body<M, M, -1, M>(kt, fa, fb, acc);
+    for (; kt < b - 1; ++kt) body<M, M, -1>(kt, fa, fb, acc);
     body<M, MN, -1>(b - 1, fa, fb, acc);
   }
 
@@ -282,22 +290,23 @@ struct Pipe {
     }
     // the last run (every remaining slice in form ML), with the identity steps
     const int k0 = t2;
+    // every slice this run loads is in form ML
     if constexpr (IDENT == IDENT_NONE) {
-      for (int kt = k0; kt < KT; ++kt) body<ML, ML, -1>(kt, fa, fb, acc);
+      for (int kt = k0; kt < KT; ++kt) body<ML, ML, -1, ML>(kt, fa, fb, acc);
     } else {
       // the slices starting at diag0 cross this wave's identity tiles in
       // order (diag0 is a multiple of the wave's extent along K and lies in
       // the last run)
       constexpr int NI = IDENT == IDENT_ROW ? TMI : TMJ;
       const int kd = diag0 / BK;
-      for (int kt = k0; kt < kd; ++kt) body<ML, ML, -1>(kt, fa, fb, acc);
-      body<ML, ML, 0>(kd, fa, fb, acc);
-      body<ML, ML, 1>(kd + 1, fa, fb, acc);
+      for (int kt = k0; kt < kd; ++kt) body<ML, ML, -1, ML>(kt, fa, fb, acc);
+      body<ML, ML, 0, ML>(kd, fa, fb, acc);
+      body<ML, ML, 1, ML>(kd + 1, fa, fb, acc);
       if constexpr (NI == 4) {
-        body<ML, ML, 2>(kd + 2, fa, fb, acc);
-        body<ML, ML, 3>(kd + 3, fa, fb, acc);
+        body<ML, ML, 2, ML>(kd + 2, fa, fb, acc);
+        body<ML, ML, 3, ML>(kd + 3, fa, fb, acc);
       }
-      for (int kt = kd + NI; kt < KT; ++kt) body<ML, ML, -1>(kt, fa, fb, acc);
+      for (int kt = kd + NI; kt < KT; ++kt) body<ML, ML, -1, ML>(kt, fa, fb, acc);
     }
     wait_vm<0>();  // the refills of the last two steps land before the ring is reused
   }
