@@ -96,7 +96,7 @@ struct Pipe {
   const uint16_t* csrc_k;
   const uint16_t* csrc_t;
   int thr_r, thr_c;        // OP_SPLIT: slices kt < thr are T
-  int64_t pstride;         // elements per panel (rows * 32)
+  uint32_t pstride_b;      // bytes per panel (rows * 32 * 2; a block is below 2^31 bytes)
   int KT;
   int wave, lane, wm, wn;
   uint16_t* lds;  // ring slot s at lds + s*SLOT: row-operand slice, then column-operand slice
@@ -107,7 +107,7 @@ struct Pipe {
   int diag0;                      // K index of this wave's first identity row / column
   float id_v;                     // identity scalar
 
-  __device__ __forceinline__ uint16_t* rslot(int kt) const { return lds + (kt % NSTAGE) * SLOT; }
+  __device__ __forceinline__ uint16_t* rslot(int kt) const { return lds + (uint32_t(kt) % NSTAGE) * SLOT; }
 
   __device__ __forceinline__ bool row_is_t(int kt) const { return RK == OP_SPLIT && kt < thr_r; }
   __device__ __forceinline__ bool col_is_t(int kt) const {
@@ -125,16 +125,21 @@ struct Pipe {
   template <int Q, int RF = -1>
   __device__ __forceinline__ void issue_one(int src_kt, int slot_kt) const {
     constexpr int q = Q & 1;
-    const uint32_t dst = lds0 + (slot_kt % NSTAGE) * SLOT * 2 + (Q < 2 ? 0 : RSLICE * 2) + (2 * wave + q) * 1024;
+    const uint32_t dst =
+        lds0 + (uint32_t(slot_kt) % NSTAGE) * SLOT * 2 + (Q < 2 ? 0 : RSLICE * 2) + (2 * wave + q) * 1024;
     bool t;
     if constexpr (RF >= 0) t = Q < 2 ? row_t(RF) : col_t(RF);
     else t = Q < 2 ? row_is_t(src_kt) : col_is_t(src_kt);
     const uint16_t* srck = Q < 2 ? rsrc_k : csrc_k;
     const uint16_t* srct = Q < 2 ? rsrc_t : csrc_t;
+    // 32-bit byte offsets from the operand's base
+    const uint32_t ks = uint32_t(src_kt);
     if (t)
-      dma16(srct + src_kt * (BK * PANEL) + wave * pstride + q * 16 * PANEL, uint32_t(lane) << 4, dst);
+      dma16(reinterpret_cast<const char*>(srct) + (ks * (BK * PANEL * 2) + uint32_t(wave) * pstride_b + q * 16 * PANEL * 2),
+            uint32_t(lane) << 4, dst);
     else
-      dma16(srck + src_kt * pstride + (2 * wave + q) * 16 * PANEL, k_loff, dst);
+      dma16(reinterpret_cast<const char*>(srck) + (ks * pstride_b + uint32_t(2 * wave + q) * (16 * PANEL * 2)), k_loff,
+            dst);
   }
   __device__ __forceinline__ void issue(int src_kt, int slot_kt) const {
     issue_one<0>(src_kt, slot_kt);
@@ -368,7 +373,7 @@ __device__ __forceinline__ void mainloop_run(const uint16_t* rsrc_k, const uint1
   p.csrc_t = csrc_t;
   p.thr_r = thr_r;
   p.thr_c = thr_c;
-  p.pstride = pstride;
+  p.pstride_b = uint32_t(pstride) * 2;
   p.KT = KT;
   p.lane = threadIdx.x & 63;
   p.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // its share of the direct loads
