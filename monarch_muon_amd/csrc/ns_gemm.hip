@@ -258,13 +258,16 @@ struct Pipe {
   }
 
   // Slices a .. b-1 in form M (b > a), the last of them reading slice b in form
-  // MN.  The steps that load a slice of the same run know its form.
+  // MN.  Runs start and end at multiples of BM / BK = 8 slices, so the slices the
+  // last NSTAGE - 1 steps load lie in the next run (form MN) and every load's
+  // form is known at compile time.
+  static_assert(BM / BK >= NSTAGE - 1, "a run is longer than the loads in flight");
   template <int M, int MN>
   __device__ __forceinline__ void run_span(int a, int b, Frags& fa, Frags& fb, f32x16 (&acc)[TMI][TMJ]) const {
     int kt = a;
     for (; kt < b - (NSTAGE - 1); ++kt) body<M, M, -1, M>(kt, fa, fb, acc);
-    for (; kt < b - 1; ++kt) body<M, M, -1>(kt, fa, fb, acc);
-    body<M, MN, -1>(b - 1, fa, fb, acc);
+    for (; kt < b - 1; ++kt) body<M, M, -1, MN>(kt, fa, fb, acc);
+    body<M, MN, -1, MN>(b - 1, fa, fb, acc);
   }
 
   __device__ __forceinline__ void run(f32x16 (&acc)[TMI][TMJ]) const {
