@@ -1,0 +1,103 @@
+"""GPU parity of each Newton-Schulz stage on its own, through mmuon_ns_stage.
+
+Every stage output is compared with an fp64 product of the stage's own bf16
+inputs as the library left them in the workspace, so a stage is checked in
+isolation (the end-to-end chain is covered in test_gpu_parity.py):
+
+  SYRK  A  = s^2 X X^T          (tiles on and above the diagonal are stored)
+  POLY  P  = b A + c A A        (A's lower tiles are the transposes of its upper ones)
+  PX    X' = s (a X + P X)
+
+Bar: |stage - fp64| <= 2^-8 * max|fp64| per block (one bf16 step at the largest
+entry; bf16 output rounding is at most half of that).  Diagonal 256 x 256 tiles
+of A and P are stored in full and must be exactly symmetric.  The shapes cover
+m = 1024 (four diagonal tiles per block, whose 32 x 32 MFMA tiles the kernels
+deal over the waves), tall and wide blocks, and zero padding.
+"""
+import ctypes as C
+
+import pytest
+import torch
+
+from monarch_muon_amd import _abi
+from monarch_muon_amd.plan import NS_COEFFS, MuonPlanner
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+TILE = 256
+SHAPES = [(2, 1024, 1024), (1, 2752, 1024), (1, 1024, 2752), (3, 512, 512), (2, 96, 136)]
+
+
+def panels(t: torch.Tensor, nblocks: int, rows: int, cols: int) -> torch.Tensor:
+    """A bf16 stack in 32-column panels ([N][cols/32][rows][32]) as row-major fp64 [N, rows, cols]."""
+    v = t.view(torch.bfloat16)[: nblocks * rows * cols].view(nblocks, cols // 32, rows, 32)
+    return v.permute(0, 2, 1, 3).reshape(nblocks, rows, cols).double().cpu()
+
+
+def mirror_upper(a: torch.Tensor) -> torch.Tensor:
+    """Full symmetric matrices from their stored 256 x 256 tiles on and above the diagonal."""
+    n = a.shape[-1] // TILE
+    out = a.clone()
+    for ti in range(n):
+        for tc in range(ti):
+            out[:, ti * TILE:(ti + 1) * TILE, tc * TILE:(tc + 1) * TILE] = \
+                a[:, tc * TILE:(tc + 1) * TILE, ti * TILE:(ti + 1) * TILE].transpose(1, 2)
+    return out
+
+
+def check_upper_tiles(got: torch.Tensor, ref: torch.Tensor, what: str) -> None:
+    n = got.shape[-1] // TILE
+    for b in range(got.shape[0]):
+        bound = 2.0 ** -8 * float(ref[b].abs().max())
+        for ti in range(n):
+            for tc in range(ti, n):
+                sl = (b, slice(ti * TILE, (ti + 1) * TILE), slice(tc * TILE, (tc + 1) * TILE))
+                err = float((got[sl] - ref[sl]).abs().max())
+                assert err <= bound, f"{what} block {b} tile ({ti},{tc}): max error {err:.3e} > {bound:.3e}"
+            d = got[b, ti * TILE:(ti + 1) * TILE, ti * TILE:(ti + 1) * TILE]
+            assert torch.equal(d, d.T), f"{what} block {b} diagonal tile {ti} is not exactly symmetric"
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_stage_outputs_against_fp64_products(shape):
+    gen = torch.Generator().manual_seed(7)
+    g = (torch.randn(shape, generator=gen) * 1e-3).to(DEV)
+    p = torch.zeros_like(g, dtype=torch.bfloat16)
+    buf = torch.zeros_like(g)
+    (gl,) = MuonPlanner().plan([p], [g.bfloat16()], [buf], torch.bfloat16)
+    lib, stream = _abi.lib(), _abi.stream_handle(DEV)
+    coeffs = (C.c_float * 3)(*NS_COEFFS)
+    a_c, b_c, c_c = NS_COEFFS
+    lay, ws, nb = gl.ws.layout, gl.ws, gl.nblocks
+    mp, np_ = lay.mp, lay.np_
+
+    def stage(it, st):
+        _abi.check(lib.mmuon_ns_stage(C.byref(gl.struct), it, 5, st, coeffs, C.c_float(0.0), _abi.NS_NO_APPLY,
+                                      stream), "mmuon_ns_stage")
+        torch.cuda.synchronize()
+
+    _abi.check(lib.mmuon_momentum_pack(C.byref(gl.struct), 0.0, stream), "pack")  # X = bf16(g), s = 1/||X||
+    torch.cuda.synchronize()
+    s = ws.scale.double().cpu().view(nb, 1, 1)
+    x = panels(ws.x0, nb, mp, np_)
+
+    stage(0, 0)  # SYRK of the first iteration (scaled by s^2)
+    a = panels(ws.a, nb, mp, mp)
+    check_upper_tiles(a, s * s * (x @ x.transpose(1, 2)), "SYRK")
+
+    stage(0, 1)  # POLY from the stored A
+    full_a = mirror_upper(a)
+    pm = panels(ws.p, nb, mp, mp)
+    check_upper_tiles(pm, b_c * full_a + c_c * (full_a @ full_a), "POLY")
+
+    stage(0, 2)  # PX from the stored P and X (first iteration: scaled by s)
+    full_p = mirror_upper(pm)
+    ref = s * (a_c * x + full_p @ x)
+    got = panels(ws.x1, nb, mp, np_)
+    for b in range(nb):
+        bound = 2.0 ** -8 * float(ref[b].abs().max())
+        err = float((got[b] - ref[b]).abs().max())
+        assert err <= bound, f"PX block {b}: max error {err:.3e} > {bound:.3e}"
+    # the zero padding stays zero through every stage
+    for pad in (got[:, lay.m:, :], got[:, :, lay.n:]):
+        assert pad.numel() == 0 or float(pad.abs().max()) == 0.0
