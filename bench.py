@@ -428,7 +428,8 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the single-GPU optimizer step only; multi-GPU runs are not part of "
-              "this build (see DESIGN.md for how the step would shard).", file=sys.stderr)
+              "this build (a sharded step would give each GPU its own share of the Newton-Schulz blocks).",
+              file=sys.stderr)
         sys.exit(2)
     from monarch_muon_amd.workloads import WORKLOADS, adamw_elements, muon_elements, ns_flops
     if args.workload.startswith("butterfly-"):
