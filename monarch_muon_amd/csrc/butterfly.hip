@@ -213,9 +213,14 @@ struct GPipe {
     if constexpr ((g) < TMI + TMJ) load_one<0, (g)>(kt + 1, fa);                             \
     if constexpr ((g) < SLICE_DMA) issue_one<(g)>(src, slt);                                 \
     __builtin_amdgcn_sched_barrier(0);
+    // raised wave priority from the barrier to the end of k step 1, so the
+    // SIMD's wave still in this phase wins issue over one already in the next
+    // step and catches up before the next barrier
+    __builtin_amdgcn_s_setprio(1);
     MMUON_GSTEP1(0) MMUON_GSTEP1(1) MMUON_GSTEP1(2) MMUON_GSTEP1(3)
     MMUON_GSTEP1(4) MMUON_GSTEP1(5) MMUON_GSTEP1(6) MMUON_GSTEP1(7)
 #undef MMUON_GSTEP1
+    __builtin_amdgcn_s_setprio(0);
   }
 
   __device__ __forceinline__ void run(f32x16 (&acc)[TMI][TMJ]) const {

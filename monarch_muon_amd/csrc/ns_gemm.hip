@@ -249,10 +249,17 @@ struct Pipe {
     if constexpr ((g) < TMI + TMJ && frag_on(g)) load_one<0, (g), MN>(kt + 1, fa);   \
     if constexpr ((g) < DMA) issue_one<(g), RF>(src, slot);                          \
     __builtin_amdgcn_sched_barrier(0);
+    // Raised wave priority from the barrier to the end of k step 1: a wave
+    // still in this phase (reads of slice kt+1, direct loads) wins issue over
+    // the SIMD's other wave once that one has moved on to the next step's
+    // k step 0, so the wave behind catches up before the next barrier
+    // (measured: Newton-Schulz 1-2% faster on the 6.89B groups).
+    __builtin_amdgcn_s_setprio(1);
     MMUON_STEP1(0) MMUON_STEP1(1) MMUON_STEP1(2) MMUON_STEP1(3)
     MMUON_STEP1(4) MMUON_STEP1(5) MMUON_STEP1(6) MMUON_STEP1(7)
 #undef MMUON_STEP1
 #undef MMUON_MFMA
+    __builtin_amdgcn_s_setprio(0);
     // the slot of slice kt is refilled only after the next barrier
     if constexpr (F >= 0) ident_add<F>(kt, acc);
   }
