@@ -176,8 +176,12 @@ int mmuon_adamw(const mmuon_adamw_args* a, void* stream);
 
 /* FP8-state AdamW: exp_avg (signed) and exp_avg_sq (unsigned) held as e4m3 with
    per-128 metadata; chunk_elems must be 128 (one metadata group per chunk).
-   have_state = 0: the moments start from zero (first step).
-   Replaces coat_state_muon.py:128-138 around membench :176-208. */
+   have_state = 1: the moments are dequantized to fp32 and updated in fp32.
+   have_state = 0: the moments are created in this step: they start from zero
+   in the PARAMETER dtype and every moment op rounds to it (the wrapped step
+   creates them with zeros_like(param)); the codes are not read.
+   Replaces coat_state_muon.py:126-139 around membench :176-208 /
+   pretrain :171-201. */
 typedef struct mmuon_adamw_fp8_tensor {
   float* scale_m; float* expand_m; float* sqrt_minmax_m;
   float* scale_v; float* expand_v; float* sqrt_minmax_v;

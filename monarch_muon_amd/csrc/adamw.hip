@@ -105,7 +105,10 @@ int launch_adamw(const AdamWArgs& a, int param_dtype, int grad_dtype, int state_
 // FP8-state AdamW: one 128-element metadata group per F8_LANES lanes,
 // F8_ELEMS (16) consecutive elements per lane; the moments are dequantized to fp32,
 // updated in fp32 (the reference's dequantized states are fp32 tensors), and
-// requantized (exp_avg signed, exp_avg_sq unsigned).
+// requantized (exp_avg signed, exp_avg_sq unsigned).  Moments created in this
+// step (have_state 0) start at zero in the parameter dtype and every moment op
+// rounds to it (TS = TP), as the wrapped step's zeros_like(param) states do
+// (coat_state_muon.py:126-139 around membench monarch_muon.py:184-190).
 // chunk = tensor << 40 | first element of the group.
 // ---------------------------------------------------------------------------
 constexpr int F8_ELEMS = 16, F8_LANES = 128 / F8_ELEMS;
@@ -141,7 +144,7 @@ __device__ __forceinline__ void store_codes(uint8_t* q, int64_t e0, int nvalid, 
     if (k < nvalid) q[e0 + k] = uint8_t(w[k >> 2] >> (8 * (k & 3)));
 }
 
-template <class TP, class TG>
+template <class TP, class TG, class TS>
 __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
   const int64_t gidx = int64_t(blockIdx.x) * F8_GPW + (threadIdx.x / F8_LANES);
   if (gidx >= a.nchunks) return;  // a group's lanes leave together
@@ -173,7 +176,7 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
     fp8_dequant_lane<F8_ELEMS>(cv, fp8_dq(Fp8Meta{M.scale_v[grp], M.expand_v[grp], M.sqrt_minmax_v[grp]}), false, v);
   }
 #pragma unroll
-  for (int k = 0; k < F8_ELEMS; ++k) adamw_elem<TP, F32T>(pv[k], clipped<TG>(gv[k], a.gscale), m[k], v[k], a);
+  for (int k = 0; k < F8_ELEMS; ++k) adamw_elem<TP, TS>(pv[k], clipped<TG>(gv[k], a.gscale), m[k], v[k], a);
   if (vec) {
     Vec8<TP>::store(p + e0, pv);
     Vec8<TP>::store(p + e0 + 8, pv + 8);
@@ -200,12 +203,14 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
 int launch_adamw_fp8(const AdamWArgs& a, int param_dtype, int grad_dtype, hipStream_t s) {
   if (a.nchunks <= 0) return 0;
   const dim3 grid(unsigned((a.nchunks + F8_GPW - 1) / F8_GPW)), block(ADAM_NT);
-  if (param_dtype == MMUON_BF16 && grad_dtype == MMUON_BF16)
-    hipLaunchKernelGGL((adamw_fp8_kernel<BF16T, BF16T>), grid, block, 0, s, a);
-  else if (param_dtype == MMUON_F32 && grad_dtype == MMUON_F32)
-    hipLaunchKernelGGL((adamw_fp8_kernel<F32T, F32T>), grid, block, 0, s, a);
-  else
+  if (param_dtype == MMUON_BF16 && grad_dtype == MMUON_BF16) {
+    if (a.have_state) hipLaunchKernelGGL((adamw_fp8_kernel<BF16T, BF16T, F32T>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((adamw_fp8_kernel<BF16T, BF16T, BF16T>), grid, block, 0, s, a);
+  } else if (param_dtype == MMUON_F32 && grad_dtype == MMUON_F32) {
+    hipLaunchKernelGGL((adamw_fp8_kernel<F32T, F32T, F32T>), grid, block, 0, s, a);
+  } else {
     return -1;
+  }
   return 0;
 }
 

@@ -58,12 +58,17 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const char* base) {
 // 16-B buffer load straight into LDS: lane l lands at lds + 16 l (M0 holds the
 // wave-uniform LDS address).  Inline assembly for the same reason as dma16: the
 // pipeline waits for exactly the slice it reads.
+// m0 is listed as clobbered (the asm writes it); clang warns that m0 is a
+// register it reserves for its own uses, which it sets right before each.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void bdma16(i32x4 rsrc, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :
                : "v"(voff), "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory");
+               : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // floor(n / d) for 0 <= n < 2^24, 1 <= d < 2^16, with magic = ceil(2^40 / d)
 // (exact because n d < 2^40).

@@ -91,12 +91,17 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // the compiler's wait-count pass does not guard every later LDS read with a
 // vmcnt(0); the pipeline waits for exactly the slice it reads (wait_vm, in-order
 // completion of vector-memory loads) and then synchronises the workgroup.
+// m0 is listed as clobbered (the asm writes it); clang warns that m0 is a
+// register it reserves for its own uses, which it sets right before each.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
                : "v"(off), "s"(base), "s"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory");
+               : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // Workgroup barrier that also stops the compiler from moving LDS reads above it.
 __device__ __forceinline__ void barrier() {

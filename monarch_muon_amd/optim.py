@@ -198,18 +198,22 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
         self._launch_adamw(params, grads, ms, vs, steps, lr, beta1, beta2, group["eps"],
                            group["weight_decay"])
 
-    def _launch_adamw(self, params, grads, ms, vs, steps, lr, beta1, beta2, eps, wd, fp8_meta=None):
+    def _launch_adamw(self, params, grads, ms, vs, steps, lr, beta1, beta2, eps, wd, fp8_meta=None, fresh=None):
+        """``fresh`` (FP8 states): per tensor, whether its moments are created
+        in this step (they start at zero in the parameter dtype)."""
+        kinds = [(s, bool(fresh[i]) if fresh is not None else False) for i, s in enumerate(steps)]
         launches = self._adam_planner.plan(params, grads, ms, vs, fp8_meta)
         lib = _abi.lib()
         for al in launches:
-            step_values = sorted({steps[i] for i in al.members})
-            if len(step_values) != 1:
-                # tensors whose step counts differ: one launch per step value
-                self._adamw_split(al, params, grads, ms, vs, steps, lr, beta1, beta2, eps, wd, fp8_meta)
+            ks = {kinds[i] for i in al.members}
+            if len(ks) != 1:
+                # tensors whose step counts (or state ages) differ: one launch per kind
+                self._adamw_split(al, params, grads, ms, vs, kinds, lr, beta1, beta2, eps, wd, fp8_meta)
                 continue
-            self._adamw_one(lib, al, step_values[0], lr, beta1, beta2, eps, wd)
+            step, new = ks.pop()
+            self._adamw_one(lib, al, step, lr, beta1, beta2, eps, wd, have_state=not new)
 
-    def _adamw_one(self, lib, al, step, lr, beta1, beta2, eps, wd):
+    def _adamw_one(self, lib, al, step, lr, beta1, beta2, eps, wd, have_state=True):
         args = _abi.AdamWArgs(tensors=al.tensors.data_ptr(), chunks=al.chunks.data_ptr(), nchunks=al.nchunks,
                               chunk_elems=al.chunk, param_dtype=_abi.dtype_code(al.pd),
                               grad_dtype=_abi.dtype_code(al.gd), state_dtype=_abi.dtype_code(al.sd),
@@ -218,21 +222,21 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
         ev = self._mark("adamw")
         if al.fp8 is not None:
             _abi.check(lib.mmuon_adamw_fp8(C.byref(args), C.cast(al.fp8.data_ptr(), C.POINTER(_abi.AdamWFp8Tensor)),
-                                           1, stream), "mmuon_adamw_fp8")
+                                           int(have_state), stream), "mmuon_adamw_fp8")
         else:
             _abi.check(lib.mmuon_adamw(C.byref(args), stream), "mmuon_adamw")
         self._mark_end(ev)
 
-    def _adamw_split(self, al, params, grads, ms, vs, steps, lr, beta1, beta2, eps, wd, fp8_meta):
+    def _adamw_split(self, al, params, grads, ms, vs, kinds, lr, beta1, beta2, eps, wd, fp8_meta):
         lib = _abi.lib()
-        by_step: dict = {}
+        by_kind: dict = {}
         for i in al.members:
-            by_step.setdefault(steps[i], []).append(i)
-        for step, idx in by_step.items():
+            by_kind.setdefault(kinds[i], []).append(i)
+        for (step, new), idx in by_kind.items():
             sub = AdamPlanner().plan([params[i] for i in idx], [grads[i] for i in idx], [ms[i] for i in idx],
                                      [vs[i] for i in idx], [fp8_meta[i] for i in idx] if fp8_meta else None)
             for sl in sub:
-                self._adamw_one(lib, sl, step, lr, beta1, beta2, eps, wd)
+                self._adamw_one(lib, sl, step, lr, beta1, beta2, eps, wd, have_state=not new)
 
     # ------------------------------------------------------------------
     # optional per-launch timing (bench.py): hipEvents on the launch stream
@@ -325,12 +329,17 @@ class CoatStateMonarchMuon(MonarchMuonOptimizer):
         params, grads = self._muon_inputs(group)
         if not params:
             return
-        bufs = [self._ensure_fp8(self.state[p], "momentum_buffer", p) for p in params]
         for p in params:
-            if (p.numel() // p.shape[0]) % 128 != 0:
+            if p.dim() != 3 or (p.numel() // p.shape[0]) % 128 != 0:
                 raise NotImplementedError("FP8 momentum needs rows*cols % 128 == 0 for every Monarch block")
+        # the wrapped step sees a dequantized (fp32) momentum, or one it creates
+        # with zeros_like(param) in the parameter dtype on a parameter's first
+        # step: that dtype keys the grouping and, with ns_dtype=None, is the
+        # Newton-Schulz dtype
+        key_dtypes = [torch.float32 if "momentum_buffer" in self.state[p] else p.dtype for p in params]
+        bufs = [self._ensure_fp8(self.state[p], "momentum_buffer", p) for p in params]
         meta = [self._meta(self.state[p], "momentum_buffer") for p in params]
-        launches = self._muon_planner.plan(params, grads, bufs, self.ns_dtype, fp8_meta=meta)
+        launches = self._muon_planner.plan(params, grads, bufs, self.ns_dtype, fp8_meta=meta, key_dtypes=key_dtypes)
         momentum = float(group["momentum"])
         lib = _abi.lib()
         for gl in launches:
@@ -350,9 +359,13 @@ class CoatStateMonarchMuon(MonarchMuonOptimizer):
         params = [p for p in group["params"] if p.grad is not None]
         if not params:
             return
+        fresh = []
         for p in params:
             _require_gpu(p)
             state = self.state[p]
+            # moments created in this step start at zero in the parameter dtype
+            # (zeros_like(param) in the wrapped step) and are rounded to it
+            fresh.append("exp_avg" not in state)
             if "step" not in state:
                 state["step"] = 0
             state["step"] += 1
@@ -368,7 +381,7 @@ class CoatStateMonarchMuon(MonarchMuonOptimizer):
         else:
             steps = [self.state[params[0]]["step"]] * len(params)
         self._launch_adamw(params, grads, ms, vs, steps, lr, beta1, beta2, group["eps"],
-                           group["weight_decay"], fp8_meta=meta)
+                           group["weight_decay"], fp8_meta=meta, fresh=fresh)
 
     def load_state_dict(self, state_dict):
         # torch.optim casts floating state to the parameter dtype; put the FP8

@@ -15,6 +15,7 @@ import math
 from collections import OrderedDict
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from . import _abi
@@ -39,8 +40,33 @@ def plan_groups(bufs) -> "OrderedDict[tuple, list[int]]":
 
 
 def _h2d_int64(values, device) -> torch.Tensor:
-    host = torch.tensor(values, dtype=torch.int64).pin_memory()
+    if isinstance(values, np.ndarray):
+        host = torch.from_numpy(np.ascontiguousarray(values, dtype=np.int64)).pin_memory()
+    else:
+        host = torch.tensor(values, dtype=torch.int64).pin_memory()
     return host.to(device, non_blocking=True)
+
+
+def _chunk_codes(numels, chunk: int) -> np.ndarray:
+    """``tensor << 40 | first element`` of every ``chunk``-element chunk of the
+    listed tensors, tensors in order (int64)."""
+    n = np.asarray(numels, dtype=np.int64)
+    per = (n + chunk - 1) // chunk
+    total = int(per.sum())
+    t = np.repeat(np.arange(n.size, dtype=np.int64), per)
+    start = (np.arange(total, dtype=np.int64) - np.repeat(np.cumsum(per) - per, per)) * chunk
+    return (t << 40) | start
+
+
+class _KeyView:
+    """A momentum buffer seen with another dtype for grouping (FP8 states are
+    grouped by the dtype the wrapped reference step sees)."""
+
+    def __init__(self, buf: torch.Tensor, dtype: torch.dtype):
+        self.device, self.dtype, self.shape = buf.device, dtype, buf.shape
+
+    def dim(self) -> int:
+        return len(self.shape)
 
 
 @dataclass
@@ -67,8 +93,8 @@ class Workspace:
         """The X stack (``which`` = 0 or 1) as ``[N, mp, np]``.  fp32 stacks are
         row-major (a view); bf16 stacks are stored in 32-column panels
         (``[N][np/32][mp][32]``) and come back as a row-major copy."""
-        t = (self.x0 if which == 0 else self.x1).view(dtype)
         mp, np_ = self.layout.mp, self.layout.np_
+        t = (self.x0 if which == 0 else self.x1).view(dtype)[:nblocks * mp * np_]
         if dtype == torch.float32:
             return t.view(nblocks, mp, np_)
         return t.view(nblocks, np_ // 32, mp, 32).permute(0, 2, 1, 3).reshape(nblocks, mp, np_)
@@ -112,27 +138,40 @@ class MuonPlanner:
         self._groups = []
         self._ws = {}
 
-    def plan(self, params, grads, bufs, ns_dtype: torch.dtype, fp8_meta=None) -> list[GroupLaunch]:
+    def plan(self, params, grads, bufs, ns_dtype: torch.dtype, fp8_meta=None, key_dtypes=None) -> list[GroupLaunch]:
+        """Launch plan of one step.  ``key_dtypes`` (FP8 states): per parameter,
+        the dtype the wrapped reference step sees for its momentum -- fp32 once
+        dequantized, the parameter dtype when the buffer is created in this
+        step -- used for the grouping key and, with ``ns_dtype=None``, as the
+        Newton-Schulz dtype."""
         sig = tuple((p.data_ptr(), g.data_ptr(), b.data_ptr(), p.dtype, g.dtype, b.dtype, tuple(b.shape))
                     for p, g, b in zip(params, grads, bufs))
         if fp8_meta is not None:
-            sig = sig + tuple(m[0].data_ptr() for m in fp8_meta)
+            sig = sig + tuple(t.data_ptr() for m in fp8_meta for t in m)
+        if key_dtypes is not None:
+            sig = sig + tuple(key_dtypes)
         if sig == self._sig:
             return self._groups
+        keys = bufs if key_dtypes is None else [_KeyView(b, d) for b, d in zip(bufs, key_dtypes)]
         self._groups = [self._build(key, idx, params, grads, bufs, ns_dtype, fp8_meta)
-                        for key, idx in plan_groups(bufs).items()]
+                        for key, idx in plan_groups(keys).items()]
         self._sig = sig
         return self._groups
 
     def _workspace(self, rows, cols, ns_code, nblocks, device) -> Workspace:
-        k = (rows, cols, ns_code, nblocks, device)
+        """One workspace per (geometry, NS dtype, device), grown to the largest
+        group seen.  Groups of one step run one after another on one stream, so
+        two groups of the same geometry share it safely."""
+        k = (rows, cols, ns_code, device)
         ws = self._ws.get(k)
-        if ws is None:
+        if ws is None or ws.scale.numel() < nblocks:
+            self._ws[k] = None  # drop the smaller one before allocating
             ws = self._ws[k] = Workspace.allocate(rows, cols, ns_code, nblocks, device)
         return ws
 
     def _build(self, key, idx, params, grads, bufs, ns_dtype, fp8_meta) -> GroupLaunch:
-        device, bdtype, rows, cols = key
+        device, kdtype, rows, cols = key
+        bdtype = bufs[idx[0]].dtype
         rc = rows * cols
         pd, gd = params[idx[0]].dtype, grads[idx[0]].dtype
         for i in idx:
@@ -145,26 +184,25 @@ class MuonPlanner:
                 raise ValueError("param, grad and momentum shapes differ")
         if ns_dtype is not None:
             ns_code = _abi.dtype_code(ns_dtype)
-        elif bdtype == torch.float8_e4m3fn:
+        elif kdtype == torch.float8_e4m3fn:
             ns_code = _abi.F32          # the FP8 reference dequantizes the momentum to fp32
         else:
-            ns_code = _abi.dtype_code(bdtype)
-        nblocks = sum(bufs[i].shape[0] for i in idx)
+            ns_code = _abi.dtype_code(kdtype)
+        counts = np.array([bufs[i].shape[0] for i in idx], dtype=np.int64)
+        nblocks = int(counts.sum())
         ws = self._workspace(rows, cols, ns_code, nblocks, device)
-        es_p, es_g, es_b = params[idx[0]].element_size(), grads[idx[0]].element_size(), bufs[idx[0]].element_size()
-        rows_tab, rows_fp8 = [], []
-        aligned = True
-        for i in idx:
-            pp, gp, bp = params[i].data_ptr(), grads[i].data_ptr(), bufs[i].data_ptr()
-            for k in range(bufs[i].shape[0]):
-                trip = (pp + k * rc * es_p, gp + k * rc * es_g, bp + k * rc * es_b)
-                aligned = aligned and all(v % 16 == 0 for v in trip)
-                rows_tab.append(trip)
-                if fp8_meta is not None:
-                    gpb = rc // 128
-                    rows_fp8.append(tuple(m.data_ptr() + k * gpb * 4 for m in fp8_meta[i]))
+        es = np.array([params[idx[0]].element_size(), grads[idx[0]].element_size(),
+                       bufs[idx[0]].element_size()], dtype=np.int64) * rc
+        bases = np.array([(params[i].data_ptr(), grads[i].data_ptr(), bufs[i].data_ptr()) for i in idx],
+                         dtype=np.int64)
+        k = np.arange(nblocks, dtype=np.int64) - np.repeat(np.cumsum(counts) - counts, counts)
+        rows_tab = np.repeat(bases, counts, axis=0) + k[:, None] * es[None, :]
+        aligned = not bool(np.any(rows_tab % 16))
         table = _h2d_int64(rows_tab, device)
-        fp8_table = _h2d_int64(rows_fp8, device) if fp8_meta is not None else None
+        fp8_table = None
+        if fp8_meta is not None:
+            mb = np.array([tuple(t.data_ptr() for t in fp8_meta[i]) for i in idx], dtype=np.int64)
+            fp8_table = _h2d_int64(np.repeat(mb, counts, axis=0) + k[:, None] * (rc // 128 * 4), device)
         gl = GroupLaunch(key, rows, cols, nblocks, list(idx), ws, table, fp8_table)
         s = gl.struct
         s.rows, s.cols, s.nblocks = rows, cols, nblocks
@@ -226,16 +264,13 @@ class AdamPlanner:
         launches = []
         chunk = 128 if fp8_meta is not None else ADAM_CHUNK
         for (device, pd, gd, sd), idx in buckets.items():
-            tens, chunks, f8 = [], [], []
-            for t, i in enumerate(idx):
-                n = params[i].numel()
-                tens.append((params[i].data_ptr(), grads[i].data_ptr(), ms[i].data_ptr(), vs[i].data_ptr(), n))
-                chunks.extend((t << 40) | s for s in range(0, n, chunk))
-                if fp8_meta is not None:
-                    f8.append(tuple(x.data_ptr() for x in fp8_meta[i]))
+            tens = [(params[i].data_ptr(), grads[i].data_ptr(), ms[i].data_ptr(), vs[i].data_ptr(), params[i].numel())
+                    for i in idx]
+            chunks = _chunk_codes([params[i].numel() for i in idx], chunk)
+            f8 = [tuple(x.data_ptr() for x in fp8_meta[i]) for i in idx] if fp8_meta is not None else None
             launches.append(AdamLaunch(
-                idx, pd, gd, sd, _h2d_int64(tens, device), _h2d_int64(chunks or [0], device), len(chunks), chunk,
-                _h2d_int64(f8, device) if fp8_meta is not None else None))
+                idx, pd, gd, sd, _h2d_int64(tens, device), _h2d_int64(chunks if chunks.size else [0], device),
+                int(chunks.size), chunk, _h2d_int64(f8, device) if f8 is not None else None))
         self._launches = launches
         self._sig = sig
         return launches
@@ -293,17 +328,16 @@ class NormPlanner:
             if not g.is_contiguous():
                 raise ValueError("gradients must be contiguous")
         device = grads[0].device
-        tens, chunks, first = [], [], []
-        for t, g in enumerate(grads):
-            first.append(len(chunks))
-            n = g.numel()
-            tens.append((g.data_ptr(), n))
-            chunks.extend((t << 40) | s for s in range(0, n, NORM_CHUNK))
-        first.append(len(chunks))
+        numels = [g.numel() for g in grads]
+        tens = [(g.data_ptr(), n) for g, n in zip(grads, numels)]
+        chunks = _chunk_codes(numels, NORM_CHUNK)
+        per = (np.asarray(numels, dtype=np.int64) + NORM_CHUNK - 1) // NORM_CHUNK
+        first = np.concatenate([[0], np.cumsum(per)]).astype(np.int64)
         f32 = dict(dtype=torch.float32, device=device)
-        self._launch = NormLaunch(grads[0].dtype, _h2d_int64(tens, device), _h2d_int64(chunks or [0], device),
-                                  _h2d_int64(first, device), len(chunks), len(grads),
-                                  torch.empty(max(1, len(chunks)), **f32), torch.empty(max(1, len(grads)), **f32),
+        self._launch = NormLaunch(grads[0].dtype, _h2d_int64(tens, device),
+                                  _h2d_int64(chunks if chunks.size else [0], device),
+                                  _h2d_int64(first, device), int(chunks.size), len(grads),
+                                  torch.empty(max(1, int(chunks.size)), **f32), torch.empty(max(1, len(grads)), **f32),
                                   torch.empty(1, **f32), torch.empty(1, **f32))
         self._sig = sig
         return self._launch

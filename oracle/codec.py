@@ -30,40 +30,37 @@ def e4m3_encode(x: np.ndarray) -> np.ndarray:
     """fp32 -> OCP e4m3fn byte, round-to-nearest-even, saturating to +-448.
 
     Pure integer restatement of IEEE rounding (no library cast), so it can pin
-    the HIP encoder bit for bit."""
+    the HIP encoder bit for bit.  32-bit integer arithmetic throughout; the
+    subnormal branch scales by 2^9 in float32, which is exact."""
     x = np.asarray(x, dtype=np.float32)
-    bits = x.view(np.uint32).astype(np.int64)
-    sign = ((bits >> 31) & 1).astype(np.uint8) << 7
-    a = np.abs(x).astype(np.float32)
-    out = np.zeros(x.shape, dtype=np.uint8)
+    sign = ((x.view(np.uint32) >> 31).astype(np.uint8)) << 7
+    a = np.abs(x)
     nan = np.isnan(a)
-    a = np.where(nan, 0, np.minimum(a, FP8_MAX)).astype(np.float32)
-    ab = a.view(np.uint32).astype(np.int64)
+    a = np.where(nan, np.float32(0), np.minimum(a, np.float32(FP8_MAX))).astype(np.float32)
+    ab = a.view(np.int32)
     exp = (ab >> 23) - 127
-    man = ab & 0x7FFFFF
-    # normal e4m3: exponent -6..8 (bias 7), 3 mantissa bits
-    normal = exp >= -6
-    # round mantissa 23 -> 3 bits, RNE
+    # normal e4m3: exponent -6..8 (bias 7), 3 mantissa bits; round the 24-bit
+    # significand to 4 bits, ties to even
     shift = 20
-    m_full = man | 0x800000
+    m_full = (ab & 0x7FFFFF) | 0x800000
     q = m_full >> shift
     rem = m_full & ((1 << shift) - 1)
     half = 1 << (shift - 1)
-    q = q + ((rem > half) | ((rem == half) & (q & 1 == 1)))
+    q = q + ((rem > half) | ((rem == half) & ((q & 1) == 1))).astype(np.int32)
     e_n = exp + 7
     carry = q >= 16
     q = np.where(carry, q >> 1, q)
     e_n = np.where(carry, e_n + 1, e_n)
     code_n = (e_n << 3) | (q & 7)
     # subnormal: value = k * 2^-9, k = 0..7 (8 rounds up to the min normal)
-    scaled = a.astype(np.float64) * 512.0            # exact in fp64
+    scaled = a * np.float32(512.0)                    # exact: a power-of-two scaling
     k = np.floor(scaled)
-    frac = scaled - k
+    frac = scaled - k                                 # exact: k and scaled share the binade
     k = k + ((frac > 0.5) | ((frac == 0.5) & (np.mod(k, 2) == 1)))
-    code_s = k.astype(np.int64)                       # k == 8 -> 0x08 = min normal, correct
-    code = np.where(normal, code_n, code_s)
+    code_s = k.astype(np.int32)                       # k == 8 -> 0x08 = min normal, correct
+    code = np.where(exp >= -6, code_n, code_s)
     code = np.where(a == 0, 0, code)
-    out = (code.astype(np.uint8) | sign)
+    out = code.astype(np.uint8) | sign
     out = np.where(nan, np.uint8(0x7F) | sign, out)
     return out.astype(np.uint8)
 

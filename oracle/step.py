@@ -42,9 +42,14 @@ def newton_schulz_batched(B: torch.Tensor) -> torch.Tensor:
     transposed = B.shape[-2] > B.shape[-1]
     if transposed:
         B = B.transpose(-2, -1)
+    # On a GPU (tests run this restatement there to get torch's GPU rounding of
+    # Python scalars) every right operand is made contiguous: same values, and
+    # batched bf16 products with a transposed right operand are avoided.
+    lay = (lambda t: t.contiguous()) if B.is_cuda else (lambda t: t)
+    B = lay(B)
     a, b, c = NS_COEFFS
     for _ in range(NS_STEPS):
-        BBt = B @ B.transpose(-2, -1)
+        BBt = B @ lay(B.transpose(-2, -1))
         # reference: 3.4445 * B - 4.7750 * BBt @ B + 2.0315 * (BBt @ BBt) @ B
         B = a * B - (-b) * BBt @ B + c * (BBt @ BBt) @ B
     if transposed:
@@ -197,3 +202,69 @@ def newton_schulz_ortho(stack: torch.Tensor, ns_dtype=torch.bfloat16) -> torch.T
     the pretrain copy does), then ``newton_schulz_batched``."""
     x = stack if ns_dtype is None or stack.dtype == ns_dtype else stack.to(ns_dtype)
     return newton_schulz_batched(x)
+
+
+# ---------------------------------------------------------------------------
+# FP8 optimizer states (pretrain/src/models/monarch/coat_state_muon.py:117-139)
+# ---------------------------------------------------------------------------
+FP8_STATES = {"momentum_buffer": True, "exp_avg": True, "exp_avg_sq": False}   # name -> signed
+
+
+def dequantize_state(state: dict, name: str, signed: bool) -> torch.Tensor:
+    """Restates ``dequantize`` (``coat_state_muon.py:94-100``): the e4m3 payload
+    ``state[name]`` and its per-128 metadata -> an fp32 tensor of the same shape
+    on the same device."""
+    data = state[name]
+    meta = [state[f"{key}_{name}"].detach().cpu().to(torch.float32).numpy() for key in ("scale", "expand",
+                                                                                        "sqrt_minmax")]
+    from . import codec
+    out = codec.dequantize(data.detach().cpu().view(torch.uint8).numpy().reshape(-1), *meta, signed)
+    return torch.from_numpy(out).reshape(data.shape).to(data.device)
+
+
+def quantize_state(state: dict, name: str, value: torch.Tensor, signed: bool) -> None:
+    """Restates ``quantize_`` (``coat_state_muon.py:103-114``): store ``value``
+    (any float dtype; the kernel loads it as fp32) as e4m3 codes plus fp32
+    ``scale_/expand_/sqrt_minmax_<name>``."""
+    from . import codec
+    codes, scale, expand, smm = codec.quantize(value.detach().to(torch.float32).cpu().numpy().reshape(-1), signed)
+    dev = value.device
+    state[name] = torch.from_numpy(codes).view(torch.float8_e4m3fn).reshape(value.shape).to(dev)
+    for key, t in zip(("scale", "expand", "sqrt_minmax"), (scale, expand, smm)):
+        state[f"{key}_{name}"] = torch.from_numpy(t).to(dev)
+
+
+class ReferenceCoatStateMonarchMuon(ReferenceMonarchMuon):
+    """CPU restatement of ``CoatStateMonarchMuon.step`` (``coat_state_muon.py:126-139``).
+
+    Every state present before the step is dequantized to fp32, the unchanged
+    step runs (``variant`` selects the copy it wraps: ``pretrain`` is the
+    reference's own class; ``membench`` wraps the bf16-Newton-Schulz copy the
+    same way), and every state of a parameter that had a gradient is quantized
+    back.  A state created during the step is created by the wrapped copy with
+    ``zeros_like(param)`` -- in the PARAMETER dtype -- so on a parameter's first
+    step the momentum, the Newton-Schulz input (pretrain copy) and the AdamW
+    moments are computed in that dtype and quantized from it; on later steps
+    the dequantized states are fp32."""
+
+    keep_values = False   # tests: keep each state's value before it is quantized
+
+    @torch.no_grad()
+    def step(self, closure=None):
+        active = [p for group in self.param_groups for p in group["params"] if p.grad is not None]
+        for p in active:
+            state = self.state[p]
+            for name, signed in FP8_STATES.items():
+                if name in state:
+                    state[name] = dequantize_state(state, name, signed)
+        loss = super().step(closure)
+        self.values = {}
+        for p in active:
+            state = self.state[p]
+            for name, signed in FP8_STATES.items():
+                if name in state:
+                    value = state.pop(name)
+                    if self.keep_values:
+                        self.values.setdefault(p, {})[name] = value
+                    quantize_state(state, name, value, signed)
+        return loss

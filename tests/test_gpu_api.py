@@ -1,0 +1,138 @@
+"""The optimizer API the reference's callers use, on the GPU.
+
+- ``step(closure)`` evaluates the closure with gradients enabled and returns
+  its loss (membench ``monarch_muon.py:114-128``);
+- under ``LambdaLR`` (``pretrain/src/optim/utils.py:63-72``) every group gains
+  ``initial_lr`` and an lr changed between steps reaches the kernels;
+- resume (``pretrain/src/optim/utils.py:103-132``; FP8 states:
+  ``pretrain/tests/test_coat_state_muon.py:80-97``): a state_dict saved after
+  step 2 and loaded into a fresh optimizer gives a step 3 bit-identical to the
+  uninterrupted run's.
+"""
+import io
+
+import pytest
+import torch
+
+from golden_inputs import CASES, make_case
+from monarch_muon_amd import CoatStateMonarchMuon, MonarchMuonOptimizer, QuantizationConfig
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def _opt(case, muon, adamw, fp8, lr=0.02):
+    ns = torch.bfloat16 if case["variant"] == "membench" else None
+    if fp8:
+        return CoatStateMonarchMuon(muon, adamw, lr=lr, momentum=0.95, qargs=QuantizationConfig(), ns_dtype=ns)
+    return MonarchMuonOptimizer(muon, adamw, lr=lr, momentum=0.95, ns_dtype=ns)
+
+
+def _bits(t):
+    return t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t
+
+
+def test_step_closure_returns_loss_and_uses_its_gradients():
+    case = CASES[1]
+    muon, adamw, _ = make_case(case, device=DEV)
+    m2, a2, _ = make_case(case, device=DEV)
+    for p in muon + adamw:
+        p.grad = None
+    calls = []
+
+    def closure():
+        assert torch.is_grad_enabled()
+        loss = sum((p.float() ** 2).sum() for p in muon + adamw)
+        loss.backward()
+        calls.append(1)
+        return loss
+
+    opt = MonarchMuonOptimizer(muon, adamw, lr=0.02)
+    loss = opt.step(closure)
+    assert calls == [1] and torch.is_tensor(loss) and loss.requires_grad
+    # the same step with the closure's gradients computed beforehand
+    for p in m2 + a2:
+        p.grad = None
+    with torch.enable_grad():
+        ref_loss = sum((p.float() ** 2).sum() for p in m2 + a2)
+        ref_loss.backward()
+    ref = MonarchMuonOptimizer(m2, a2, lr=0.02)
+    assert ref.step() is None
+    torch.cuda.synchronize()
+    assert torch.equal(loss.detach(), ref_loss.detach())
+    for p, q in zip(muon + adamw, m2 + a2):
+        assert torch.equal(p, q)
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["plain", "fp8"])
+def test_lambda_lr_schedule_reaches_the_kernels(fp8):
+    case = CASES[1]
+    factors = [1.0, 0.5, 0.25]
+    muon, adamw, _ = make_case(case, device=DEV)
+    opt = _opt(case, muon, adamw, fp8)
+    sched = torch.optim.lr_scheduler.LambdaLR(opt, lambda s: factors[min(s, len(factors) - 1)])
+    assert all(g["initial_lr"] == 0.02 for g in opt.param_groups)
+    sd = opt.state_dict()
+    assert all(g["initial_lr"] == 0.02 for g in sd["param_groups"])
+    m2, a2, _ = make_case(case, device=DEV)
+    ref = _opt(case, m2, a2, fp8)
+    for f in factors:
+        assert all(g["lr"] == pytest.approx(0.02 * f) for g in opt.param_groups)
+        opt.step()
+        sched.step()
+        for g in ref.param_groups:
+            g["lr"] = 0.02 * f
+        ref.step()
+    torch.cuda.synchronize()
+    for p, q in zip(muon + adamw, m2 + a2):
+        assert torch.equal(p, q)
+    # a different lr gives different weights: the value is not ignored
+    m3, a3, _ = make_case(case, device=DEV)
+    other = _opt(case, m3, a3, fp8)
+    for _ in factors:
+        other.step()
+    torch.cuda.synchronize()
+    assert not torch.equal(muon[0], m3[0])
+
+
+@pytest.mark.parametrize("case_idx,fp8", [(1, False), (2, False), (1, True), (2, True)],
+                         ids=["membench-bf16", "pretrain-fp32", "membench-bf16-fp8", "pretrain-fp32-fp8"])
+def test_resume_after_step_two_equals_uninterrupted(case_idx, fp8):
+    case = CASES[case_idx]
+    muon, adamw, _ = make_case(case, device=DEV)
+    opt = _opt(case, muon, adamw, fp8)
+    sched = torch.optim.lr_scheduler.LambdaLR(opt, lambda s: 1.0 / (1 + s))
+    for _ in range(2):
+        opt.step()
+        sched.step()
+    torch.cuda.synchronize()
+    snapshot = [p.detach().clone() for p in muon + adamw]
+    buf = io.BytesIO()
+    torch.save({"optimizer": opt.state_dict(), "scheduler": sched.state_dict()}, buf)
+    opt.step()                                              # uninterrupted step 3
+    torch.cuda.synchronize()
+
+    buf.seek(0)
+    ckpt = torch.load(buf, weights_only=True)
+    m2, a2, _ = make_case(case, device=DEV)
+    with torch.no_grad():
+        for p, s in zip(m2 + a2, snapshot):
+            p.copy_(s)
+    opt2 = _opt(case, m2, a2, fp8)
+    sched2 = torch.optim.lr_scheduler.LambdaLR(opt2, lambda s: 1.0 / (1 + s))
+    opt2.load_state_dict(ckpt["optimizer"])
+    sched2.load_state_dict(ckpt["scheduler"])
+    assert [g["lr"] for g in opt2.param_groups] == [g["lr"] for g in opt.param_groups]
+    opt2.step()                                             # resumed step 3
+    torch.cuda.synchronize()
+    for p, q in zip(muon + adamw, m2 + a2):
+        assert torch.equal(p, q)
+    for p, q in zip(muon + adamw, m2 + a2):
+        s1, s2 = opt.state[p], opt2.state[q]
+        assert set(s1) == set(s2)
+        for k in s1:
+            if torch.is_tensor(s1[k]):
+                assert s1[k].dtype == s2[k].dtype, k
+                assert torch.equal(_bits(s1[k]), _bits(s2[k])), k
+            else:
+                assert s1[k] == s2[k], k

@@ -227,17 +227,165 @@ def test_codec_special_groups():
     assert smm[0] == np.float32(10.0)
 
 
-def test_codec_halving_invariant():
-    # test_coat_state_muon.py:40-51: dequantize, halve exactly, requantize gives the
-    # codes and metadata of quantizing the halved values directly
+def test_codec_group_max_encodes_to_fp8_max():
+    # q = sign * (|x|/smm)^e / ((absmax/smm)^e / 448): the largest |value| of every
+    # group lands on +-448 (code 0x7E), which pins scale against expand and smm
     x = _decades(1000 * 129, 10)
     for signed in (True, False):
         v = x if signed else x * x
         q, sc, ex, smm = codec.quantize(v, signed)
+        g = (v.size + 127) // 128
+        pad = np.zeros(g * 128, dtype=np.float32)
+        pad[:v.size] = v
+        top = np.argmax(np.abs(pad.reshape(g, 128)), axis=1) + np.arange(g) * 128
+        assert np.all(q[top] & 0x7F == 0x7E)
+        assert np.all((q[top] >> 7) == (pad[top] < 0))
+        # and it decodes back to that value within e4m3 + power rounding
         d = codec.dequantize(q, sc, ex, smm, signed)
-        a = codec.quantize(d * np.float32(0.5), signed)
-        b = codec.quantize((d * np.float32(0.5)).astype(np.float32), signed)
-        for u, w in zip(a, b):
-            np.testing.assert_array_equal(u, w)
-        # halving a group leaves its expansion unchanged and halves sqrt_minmax
-        np.testing.assert_array_equal(a[2], codec.quantize(d, signed)[2])
+        np.testing.assert_allclose(d[top], pad[top], rtol=1e-5)
+
+
+def test_codec_power_of_four_homogeneity():
+    # scaling a group by 4 (or 1/4) scales absmax, absmin and sqrt(absmax)*sqrt(absmin)
+    # exactly (sqrt(4a) = 2 sqrt(a) in IEEE arithmetic), so codes, scale and expand
+    # are unchanged and sqrt_minmax is scaled by exactly 4; the decoder is linear in it
+    x = _decades(1000 * 129, 11)
+    for signed in (True, False):
+        v = x if signed else x * x
+        q, sc, ex, smm = codec.quantize(v, signed)
+        for f in (np.float32(4.0), np.float32(0.25)):
+            q2, sc2, ex2, smm2 = codec.quantize(v * f, signed)
+            np.testing.assert_array_equal(q2, q)
+            np.testing.assert_array_equal(sc2, sc)
+            np.testing.assert_array_equal(ex2, ex)
+            np.testing.assert_array_equal(smm2, smm * f)
+        d = codec.dequantize(q, sc, ex, smm, signed)
+        np.testing.assert_array_equal(codec.dequantize(q, sc, ex, smm * np.float32(4), signed), d * np.float32(4))
+
+
+def test_codec_halving_after_dequantize():
+    # the pattern of test_coat_state_muon.py:40-51 (dequantize, halve exactly,
+    # requantize): the halved group keeps its codes and expansion, and its
+    # sqrt_minmax and scale move by at most an ulp or two (sqrt(a/2) is not
+    # exactly sqrt(a)/sqrt(2))
+    x = _decades(1000 * 129, 12)
+    for signed in (True, False):
+        v = x if signed else x * x
+        d = codec.dequantize(*codec.quantize(v, signed), signed)
+        full = codec.quantize(d, signed)
+        half = codec.quantize(d * np.float32(0.5), signed)
+        np.testing.assert_array_equal(half[0], full[0])
+        np.testing.assert_array_equal(half[2], full[2])
+        np.testing.assert_allclose(half[3], full[3] * np.float32(0.5), rtol=3e-7, atol=0)
+        # scale = (absmax/smm)^expand / 448: an ulp of smm plus the division's
+        # rounding move the base by up to ~1.5 ulps, which the power multiplies
+        # by expand; pow and the division by 448 add an ulp each
+        rel = np.abs(half[1].astype(np.float64) / full[1] - 1)
+        assert np.all(rel <= (2 * full[2].astype(np.float64) + 3) * 2.0 ** -23)
+
+
+# ---------------------------------------------------------------- FP8-state wrapper (coat_state_muon.py:117-139)
+def _coat_inputs(dtype, seed=20):
+    g = torch.Generator().manual_seed(seed)
+    shapes = [(2, 64, 64), (1, 128, 64), (1, 64, 128)]
+    muon = []
+    for s in shapes:
+        p = (torch.randn(s, generator=g) * 0.02).to(dtype).requires_grad_(True)
+        p.grad = (torch.randn(s, generator=g) * 1e-3).to(dtype)
+        muon.append(p)
+    a = (torch.randn(100, 64, generator=g) * 0.02).to(dtype).requires_grad_(True)
+    a.grad = (torch.randn(100, 64, generator=g) * 1e-3).to(dtype)
+    return muon, [a]
+
+
+def _clone(ps):
+    out = []
+    for p in ps:
+        q = p.detach().clone().requires_grad_(True)
+        q.grad = p.grad.clone()
+        out.append(q)
+    return out
+
+
+COAT_CASES = [("pretrain", torch.float32), ("pretrain", torch.bfloat16), ("membench", torch.bfloat16)]
+
+
+@pytest.mark.parametrize("variant,dtype", COAT_CASES)
+def test_coat_oracle_first_step_is_unwrapped_step_then_quantize(variant, dtype):
+    from oracle.step import FP8_STATES, ReferenceCoatStateMonarchMuon
+    muon, adamw = _coat_inputs(dtype)
+    m2, a2 = _clone(muon), _clone(adamw)
+    wrapped = ReferenceCoatStateMonarchMuon(muon, adamw, lr=0.02, variant=variant)
+    plain = ReferenceMonarchMuon(m2, a2, lr=0.02, variant=variant)
+    wrapped.step()
+    plain.step()
+    for p, q in zip(muon + adamw, m2 + a2):
+        assert torch.equal(p, q)                     # quantization happens after the step
+        for name, signed in FP8_STATES.items():
+            if name not in plain.state[q]:
+                continue
+            value = plain.state[q][name]
+            assert value.dtype == dtype              # created by zeros_like(param)
+            codes, sc, ex, smm = codec.quantize(value.float().numpy(), signed)
+            st = wrapped.state[p]
+            assert st[name].dtype == torch.float8_e4m3fn
+            np.testing.assert_array_equal(st[name].view(torch.uint8).numpy().reshape(-1), codes)
+            for key, ref in zip(("scale", "expand", "sqrt_minmax"), (sc, ex, smm)):
+                assert st[f"{key}_{name}"].dtype == torch.float32
+                np.testing.assert_array_equal(st[f"{key}_{name}"].numpy(), ref)
+
+
+@pytest.mark.parametrize("variant,dtype", COAT_CASES)
+def test_coat_oracle_later_step_runs_on_fp32_dequantized_states(variant, dtype):
+    from oracle.step import ReferenceCoatStateMonarchMuon
+    muon, adamw = _coat_inputs(dtype, seed=21)
+    wrapped = ReferenceCoatStateMonarchMuon(muon, adamw, lr=0.02, variant=variant)
+    wrapped.step()
+    # an unwrapped copy started from the decoded states (decoded here, with the
+    # signedness spelled out per state) must take the same second step
+    m2, a2 = _clone(muon), _clone(adamw)
+    plain = ReferenceMonarchMuon(m2, a2, lr=0.02, variant=variant)
+    decode = lambda st, n, s: torch.from_numpy(codec.dequantize(
+        st[n].view(torch.uint8).numpy().reshape(-1), st[f"scale_{n}"].numpy(), st[f"expand_{n}"].numpy(),
+        st[f"sqrt_minmax_{n}"].numpy(), s)).reshape(st[n].shape)
+    for p, q in zip(muon, m2):
+        plain.state[q]["momentum_buffer"] = decode(wrapped.state[p], "momentum_buffer", True)
+    for p, q in zip(adamw, a2):
+        st = wrapped.state[p]
+        plain.state[q].update(step=st["step"], exp_avg=decode(st, "exp_avg", True),
+                              exp_avg_sq=decode(st, "exp_avg_sq", False))
+    wrapped.step()
+    plain.step()
+    for p, q in zip(muon + adamw, m2 + a2):
+        assert torch.equal(p, q)
+    for p, q in zip(muon, m2):
+        assert plain.state[q]["momentum_buffer"].dtype == torch.float32
+        codes = codec.quantize(plain.state[q]["momentum_buffer"].numpy(), True)[0]
+        np.testing.assert_array_equal(wrapped.state[p]["momentum_buffer"].view(torch.uint8).numpy().reshape(-1),
+                                      codes)
+
+
+def test_coat_oracle_halving_pattern():
+    # test_coat_state_muon.py:40-51 applied to the wrapper's AdamW states: with
+    # betas (0.5, 0.5), lr 0 and zero gradients the step halves both moments
+    # exactly, so the stored states are the quantized halves of the decoded ones
+    from oracle.step import ReferenceCoatStateMonarchMuon, dequantize_state
+    _, adamw = _coat_inputs(torch.float32, seed=22)
+    opt = ReferenceCoatStateMonarchMuon([], adamw, lr=0.02, adamw_weight_decay=0.0, variant="pretrain")
+    opt.step()
+    p = adamw[0]
+    before = {n: dequantize_state(opt.state[p], n, s) for n, s in (("exp_avg", True), ("exp_avg_sq", False))}
+    for group in opt.param_groups:
+        group["betas"] = (0.5, 0.5)
+        group["lr"] = 0.0
+    p.grad.zero_()
+    w = p.detach().clone()
+    opt.step()
+    assert torch.equal(p, w)
+    for name, signed in (("exp_avg", True), ("exp_avg_sq", False)):
+        codes, sc, ex, smm = codec.quantize((before[name] * 0.5).numpy(), signed)
+        st = opt.state[p]
+        np.testing.assert_array_equal(st[name].view(torch.uint8).numpy().reshape(-1), codes)
+        np.testing.assert_array_equal(st[f"scale_{name}"].numpy(), sc)
+        np.testing.assert_array_equal(st[f"expand_{name}"].numpy(), ex)
+        np.testing.assert_array_equal(st[f"sqrt_minmax_{name}"].numpy(), smm)
