@@ -235,6 +235,21 @@ typedef struct mmuon_grad_norm_args {
 } mmuon_grad_norm_args;
 int mmuon_grad_clip_coef(const mmuon_grad_norm_args* a, void* stream);
 
+/* The same coefficient with no caller workspace: exactly mmuon_grad_clip_coef's
+   kernels and results, with a->partial and a->norms ignored (pass NULL); the
+   caller still passes the tables and the total / coef outputs.
+   No counterpart in the reference.  It is for callers that cannot allocate
+   device memory (code under HIP graph capture, tight training or serving
+   loops, harnesses that forbid hipMalloc); this call allocates nothing.  The
+   partial sums and norms live in a static array the library holds on each GPU
+   until the process ends: MMUON_NOALLOC_SCRATCH_FLOATS floats (4 MiB), enough
+   for (nchunks rounded up to 64) + ntensors; larger inputs return
+   MMUON_ERANGE.  The stream must belong to the current device.  Calls on one
+   stream are ordered; calls that overlap on one GPU (several streams or
+   threads) share the array and race. */
+#define MMUON_NOALLOC_SCRATCH_FLOATS (1 << 20)
+int mmuon_grad_clip_coef_noalloc(const mmuon_grad_norm_args* a, void* stream);
+
 /* Monarch butterfly multiply, the layer step that produces the (nb, r, c)
    gradients the optimizer consumes.  w1 (nblocks, q, p) and w2 (nblocks, s, q)
    are a MonarchLinear's blkdiag1 / blkdiag2 (k = l = nblocks, r = q);

@@ -16,7 +16,8 @@ LIB_PATH = Path(os.environ.get("MMUON_LIB", Path(__file__).resolve().parent / "l
 F32, BF16, F8E4M3 = 0, 1, 2
 GROUP_ALIGNED16 = 1
 NS_NO_APPLY = 1
-ABI_VERSION = 3
+ABI_VERSION = 4
+NOALLOC_SCRATCH_FLOATS = 1 << 20
 
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8E4M3}
 
@@ -109,6 +110,7 @@ SIGNATURES = {
     "mmuon_fp8_dequantize": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                        C.c_int64, C.c_int32, C.c_void_p]),
     "mmuon_grad_clip_coef": (C.c_int, [C.POINTER(GradNormArgs), C.c_void_p]),
+    "mmuon_grad_clip_coef_noalloc": (C.c_int, [C.POINTER(GradNormArgs), C.c_void_p]),
     "mmuon_butterfly_fwd": (C.c_int, [C.POINTER(ButterflyArgs), C.c_void_p]),
     "mmuon_butterfly_bwd": (C.c_int, [C.POINTER(ButterflyArgs), C.c_void_p]),
     "mmuon_butterfly_workspace": (C.c_size_t, [C.POINTER(ButterflyArgs)]),

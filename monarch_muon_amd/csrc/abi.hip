@@ -103,11 +103,33 @@ mmuon::PackArgs pack_args(const mmuon_group* g, const Geometry& geo, float mu, i
 
 }  // namespace
 
+namespace mmuon {
+
+int set_error(int code, const char* msg) { return fail(code, "%s", msg); }
+
+int launch_status(const char* what) { return check_launch(what); }
+
+int check_grad_norm_args(const mmuon_grad_norm_args* a, bool workspace) {
+  if (a == nullptr) return fail(MMUON_EINVAL, "null gradient-norm arguments");
+  if (a->grad_dtype != MMUON_F32 && a->grad_dtype != MMUON_BF16)
+    return fail(MMUON_EINVAL, "gradient dtype must be F32 or BF16");
+  if (a->nchunks < 0 || a->ntensors < 0) return fail(MMUON_EINVAL, "negative chunk or tensor count");
+  if (a->nchunks > 0x7fffffff) return fail(MMUON_ERANGE, "too many gradient chunks");
+  if (a->chunk_elems <= 0) return fail(MMUON_EINVAL, "chunk_elems must be positive");
+  if (!a->total || !a->coef || (a->nchunks > 0 && (!a->tensors || !a->chunks)) || !a->first_chunk)
+    return fail(MMUON_EINVAL, "null gradient-norm pointer");
+  if (workspace && (!a->norms || (a->nchunks > 0 && !a->partial)))
+    return fail(MMUON_EINVAL, "null gradient-norm workspace pointer");
+  return MMUON_OK;
+}
+
+}  // namespace mmuon
+
 extern "C" {
 
 const char* mmuon_last_error(void) { return g_err.c_str(); }
 
-int mmuon_abi_version(void) { return 3; }
+int mmuon_abi_version(void) { return 4; }
 
 int mmuon_ns_layout(int32_t rows, int32_t cols, int32_t ns_dtype, int64_t nblocks,
                     mmuon_ns_layout_t* out) {
@@ -328,15 +350,7 @@ int mmuon_fp8_dequantize(const uint8_t* codes, const float* scale, const float* 
 }
 
 int mmuon_grad_clip_coef(const mmuon_grad_norm_args* a, void* stream) {
-  if (a == nullptr) return fail(MMUON_EINVAL, "null gradient-norm arguments");
-  if (a->grad_dtype != MMUON_F32 && a->grad_dtype != MMUON_BF16)
-    return fail(MMUON_EINVAL, "gradient dtype must be F32 or BF16");
-  if (a->nchunks < 0 || a->ntensors < 0) return fail(MMUON_EINVAL, "negative chunk or tensor count");
-  if (a->nchunks > 0x7fffffff) return fail(MMUON_ERANGE, "too many gradient chunks");
-  if (a->chunk_elems <= 0) return fail(MMUON_EINVAL, "chunk_elems must be positive");
-  if (!a->total || !a->coef || !a->norms || (a->nchunks > 0 && (!a->tensors || !a->chunks || !a->partial)) ||
-      !a->first_chunk)
-    return fail(MMUON_EINVAL, "null gradient-norm pointer");
+  if (int rc = mmuon::check_grad_norm_args(a, true)) return rc;
   mmuon::launch_grad_clip_coef(*a, static_cast<hipStream_t>(stream));
   return check_launch("mmuon_grad_clip_coef");
 }

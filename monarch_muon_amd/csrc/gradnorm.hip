@@ -8,6 +8,10 @@
 // read each gradient as dtype(g * coef), so the rescale pass is not needed.
 // Reductions run in a fixed order, so the result does not vary between runs.
 // Algorithmic HBM traffic: one read of every gradient.
+#include <stdio.h>
+
+#include <mutex>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -102,4 +106,83 @@ int launch_grad_clip_coef(const mmuon_grad_norm_args& a, hipStream_t s) {
   return 0;
 }
 
+// ---------------------------------------------------------------------------
+// mmuon_grad_clip_coef_noalloc: the same three launches with the per-chunk
+// partial sums and the per-tensor norms in `scratch`, a file-scope device
+// array, instead of caller workspace.  Each GPU the library runs on holds its
+// own copy (MMUON_NOALLOC_SCRATCH_FLOATS floats) until the process ends; in
+// host code `scratch` names a host-side stand-in, so its device address is
+// looked up once per device (hipGetSymbolAddress, with that device current)
+// and only that address is handed to kernels.  Every partial and norm is
+// written before it is read within one call, so nothing needs clearing; calls
+// that overlap on one GPU (other streams, other threads) share the array and
+// race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[MMUON_NOALLOC_SCRATCH_FLOATS];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, once looked up
+
+int scratch_address(int dev, float** out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      char msg[256];
+      snprintf(msg, sizeof msg, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+      return set_error(MMUON_EHIP, msg);
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return MMUON_OK;
+}
+
+}  // namespace
 }  // namespace mmuon
+
+extern "C" int mmuon_grad_clip_coef_noalloc(const mmuon_grad_norm_args* a, void* stream) {
+  using namespace mmuon;
+  if (int rc = check_grad_norm_args(a, false)) return rc;
+  // partials [0, nchunks), norms from the next 256-B boundary
+  const int64_t norms_at = (a->nchunks + 63) / 64 * 64;
+  const int64_t need = norms_at + a->ntensors;
+  char msg[256];
+  if (need > MMUON_NOALLOC_SCRATCH_FLOATS) {
+    snprintf(msg, sizeof msg,
+             "needs %lld floats of scratch (%lld chunks, %d tensors); the no-allocation entry point holds %d",
+             (long long)need, (long long)a->nchunks, a->ntensors, MMUON_NOALLOC_SCRATCH_FLOATS);
+    return set_error(MMUON_ERANGE, msg);
+  }
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    snprintf(msg, sizeof msg, "hipGetDevice: %s", hipGetErrorString(e));
+    return set_error(MMUON_EHIP, msg);
+  }
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (s != nullptr) {
+    hipDevice_t sd = 0;
+    e = hipStreamGetDevice(s, &sd);
+    if (e != hipSuccess) {
+      snprintf(msg, sizeof msg, "hipStreamGetDevice: %s", hipGetErrorString(e));
+      return set_error(MMUON_EHIP, msg);
+    }
+    if (int(sd) != dev) {
+      snprintf(msg, sizeof msg, "the stream belongs to device %d but device %d is current", int(sd), dev);
+      return set_error(MMUON_EINVAL, msg);
+    }
+  }
+  if (dev < 0 || dev >= kMaxDevices) return set_error(MMUON_ERANGE, "device index beyond 63");
+  float* base = nullptr;
+  if (int rc = scratch_address(dev, &base)) return rc;
+  mmuon_grad_norm_args k = *a;
+  k.partial = base;
+  k.norms = base + norms_at;
+  launch_grad_clip_coef(k, s);
+  return launch_status("mmuon_grad_clip_coef_noalloc");
+}

@@ -72,6 +72,14 @@ int launch_adamw_fp8(const AdamWArgs& a, int param_dtype, int grad_dtype, hipStr
 
 // Gradient-norm clipping coefficient --------------------------------------------
 int launch_grad_clip_coef(const mmuon_grad_norm_args& a, hipStream_t s);
+// argument checks shared by the two entry points (workspace: partial and norms
+// must be given)
+int check_grad_norm_args(const mmuon_grad_norm_args* a, bool workspace);
+
+// Error reporting shared by the translation units: set the thread-local
+// message of mmuon_last_error and return code; the status of the last launch.
+int set_error(int code, const char* msg);
+int launch_status(const char* what);
 
 // Monarch butterfly multiply -------------------------------------------------------
 size_t butterfly_workspace(const mmuon_butterfly_args& a);
