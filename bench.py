@@ -2,6 +2,8 @@
 
     python bench.py [--steps K] [--warmup W] [--workload 6.89b-nb4] [--no-cpu-baseline]
     python bench.py --workload butterfly-6.89b [--tokens 4096]
+    python bench.py --hbm-ceiling          # read / write / copy bandwidth of this GPU
+    python bench.py --power                # socket power and GFX clock per step kernel
 
 Runs the full ``MonarchMuonOptimizer.step()`` (Muon group: momentum, bf16
 Newton-Schulz over every Monarch block, apply; AdamW group) of the named
@@ -10,6 +12,11 @@ between two device synchronisations, and prints one JSON line.  The dominant
 kernel's roofline comes from per-launch hipEvents on the launch stream over
 extra instrumented steps; the CPU baseline times the oracle (the CPU
 restatement of the reference step) on a bounded sample of the same workload.
+
+After the timed steps, a second leg replaces every gradient with a freshly
+allocated tensor before each step, as ``zero_grad(set_to_none=True)`` and the
+next backward do in the reference's training loop, and reports the host time
+the launch planners spend rebuilding their pointer tables (``host_plan_ms``).
 
 ``--workload butterfly-<model>`` times the Monarch butterfly multiply instead:
 forward + backward of one transformer layer's seven Monarch projections
@@ -193,21 +200,53 @@ def hbm_traffic(workload, kernel):
 
 
 # ---------------------------------------------------------------- CPU baseline
+CPU_SAMPLE_LAYERS = 4
+
+
+def host_cpu_info(threads):
+    """What the CPU baseline ran on: model string, logical CPUs this process
+    may use, the physical cores behind them, and the threads used."""
+    model, cores = "", set()
+    cur = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if not line.strip():
+                    if "processor" in cur:
+                        cores.add((int(cur["processor"]), cur.get("physical id", "0"), cur.get("core id", cur["processor"])))
+                    cur = {}
+                    continue
+                k, _, v = line.partition(":")
+                cur[k.strip()] = v.strip()
+                if k.strip() == "model name" and not model:
+                    model = v.strip()
+            if "processor" in cur:
+                cores.add((int(cur["processor"]), cur.get("physical id", "0"), cur.get("core id", cur["processor"])))
+    except OSError:
+        pass
+    allowed = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    phys = {(pid, cid) for proc, pid, cid in cores if proc in allowed}
+    return {"cpu_model": model, "threads": threads, "logical_cpus_allowed": len(allowed),
+            "physical_cores_allowed": len(phys) or None, "os_cpu_count": os.cpu_count()}
+
+
 def cpu_baseline(w, seed=0):
     """The oracle step on the host cores over a bounded sample: the Muon blocks
-    of one transformer layer plus 1/n_layer of the AdamW elements; scaled by
-    n_layer to one full step."""
+    of the first CPU_SAMPLE_LAYERS transformer layers plus the same fraction of
+    the AdamW elements; scaled to one full step."""
     from oracle.step import ReferenceMonarchMuon
     from monarch_muon_amd.workloads import parameter_inventory
-    threads = max(1, min(16, os.cpu_count() or 1))
+    allowed = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = max(1, min(16, allowed))
     torch.set_num_threads(threads)
+    layers = min(CPU_SAMPLE_LAYERS, w.n_layer)
     gen = torch.Generator().manual_seed(seed)
     muon, adamw, bufs = [], [], []
     for name, shape, is_muon in parameter_inventory(w):
-        if ".h." in name and int(name.split(".")[2]) != 0:
+        if ".h." in name and int(name.split(".")[2]) >= layers:
             continue
         if not is_muon and len(shape) == 2:
-            shape = (max(1, shape[0] // w.n_layer), shape[1])
+            shape = (max(1, shape[0] * layers // w.n_layer), shape[1])
         p = (torch.randn(shape, generator=gen) * 0.02).to(w.param_dtype).requires_grad_(True)
         p.grad = (torch.randn(shape, generator=gen) * 1e-3).to(w.param_dtype)
         (muon if is_muon else adamw).append(p)
@@ -224,16 +263,11 @@ def cpu_baseline(w, seed=0):
         opt.step()
         times.append(time.perf_counter() - t0)
     sample_ms = statistics.median(times) * 1e3
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
-    except OSError:
-        pass
-    return {"value": round(sample_ms * w.n_layer, 1), "unit": "ms", "cores": threads, "kind": "port",
-            "sample": f"oracle step (torch CPU) over layer 0's Muon blocks + 1/{w.n_layer} of the AdamW "
-                      f"elements, median of 3 after 1 warm-up = {sample_ms:.1f} ms, x{w.n_layer} layers",
-            "cpu_model": model, "os_cpu_count": os.cpu_count()}
+    scale = w.n_layer / layers
+    return {"value": round(sample_ms * scale, 1), "unit": "ms", "cores": threads, "kind": "port",
+            "sample": f"oracle step (torch CPU) over the Muon blocks of layers 0-{layers - 1} + {layers}/{w.n_layer} "
+                      f"of the AdamW elements, median of 3 after 1 warm-up = {sample_ms:.1f} ms, x{scale:g}",
+            **host_cpu_info(threads)}
 
 
 # ---------------------------------------------------------------- butterfly
@@ -294,7 +328,8 @@ def butterfly_cpu_baseline(layer):
     """The oracle (torch CPU) forward + backward of every projection of the layer at 1/8 of the
     tokens, scaled by 8."""
     from oracle import butterfly as bf
-    threads = max(1, min(16, os.cpu_count() or 1))
+    allowed = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = max(1, min(16, allowed))
     torch.set_num_threads(threads)
     frac = 8
     cpu = [(x[: x.shape[0] // frac].cpu(), w1.cpu(), w2.cpu(), d[: d.shape[0] // frac].cpu())
@@ -312,7 +347,7 @@ def butterfly_cpu_baseline(layer):
     return {"value": round(sample_ms * frac, 1), "unit": "ms", "cores": threads, "kind": "port",
             "sample": f"oracle butterfly fwd+bwd (torch CPU, fp32 products of bf16 values) of the 7 projections "
                       f"at {cpu[0][0].shape[0]} tokens = {sample_ms:.1f} ms after 1 warm-up, x{frac}",
-            "os_cpu_count": os.cpu_count()}
+            **host_cpu_info(threads)}
 
 
 def bench_butterfly(args, w):
@@ -403,6 +438,329 @@ def bench_butterfly(args, w):
     print(json.dumps(res), flush=True)
 
 
+# ---------------------------------------------------------------- fresh gradients
+def fresh_grad_leg(opt, params, steps=5):
+    """Steps whose every gradient is a newly allocated tensor at a new address
+    (the previous step's gradients are still held while the new ones are
+    allocated), as in a training loop that drops the gradients after each step
+    (``zero_grad(set_to_none=True)``, pretrain/src/optim/base.py:125) and gets
+    new ones from the next backward.  The planners then rebuild their pointer
+    tables every step.  Returns host ms spent in the planners, host ms of the
+    whole ``step()`` call, and wall ms per step (synchronised)."""
+    saved = [p.grad for p in params]
+    spent = [0.0]
+    planners = (opt._muon_planner, opt._adam_planner)
+
+    def timed(fn):
+        def wrapper(*a, **k):
+            t0 = time.perf_counter()
+            try:
+                return fn(*a, **k)
+            finally:
+                spent[0] += time.perf_counter() - t0
+        return wrapper
+
+    for pl in planners:
+        pl.plan = timed(pl.plan)   # instance attribute shadows the method
+    plan_ms, host_ms, wall_ms = [], [], []
+    try:
+        for i in range(steps + 1):
+            fresh = [g.clone() for g in saved]
+            for p, g in zip(params, fresh):
+                p.grad = g
+            del fresh
+            torch.cuda.synchronize()
+            spent[0] = 0.0
+            t0 = time.perf_counter()
+            opt.step()
+            t1 = time.perf_counter()
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            if i:  # the leg's first step is dropped like a warm-up
+                plan_ms.append(spent[0] * 1e3)
+                host_ms.append((t1 - t0) * 1e3)
+                wall_ms.append((t2 - t0) * 1e3)
+    finally:
+        for pl in planners:
+            del pl.plan
+        for p, g in zip(params, saved):
+            p.grad = g
+    return {"host_plan_ms": round(statistics.median(plan_ms), 3),
+            "host_step_call_ms": round(statistics.median(host_ms), 3),
+            "step_ms": round(statistics.median(wall_ms), 3), "steps": steps,
+            "note": "every gradient reallocated at a new address before each step; planners rebuild their tables"}
+
+
+# ---------------------------------------------------------------- HBM ceiling
+def hbm_ceiling(args):
+    """Read, write and copy bandwidth of 16-B vector streams over 4 GiB
+    (mmuon_hbm_stream), swept over grid sizes and plain / non-temporal
+    accesses, beside torch's device copy.  Bytes moved = read + written."""
+    from monarch_muon_amd import _abi
+    lib = _abi.lib()
+    dev = torch.device("cuda", 0)
+    nbytes = 4 << 30
+    gen = torch.Generator(device=dev).manual_seed(0)
+    src = torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), dtype=torch.int32, device=dev, generator=gen)
+    dst = torch.empty_like(src)
+    stream = _abi.stream_handle(dev)
+    log(f"[bench] HBM ceiling on {torch.cuda.get_device_name(dev)}, {nbytes >> 30} GiB buffers")
+
+    def timed(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            b.synchronize()
+            ts.append(a.elapsed_time(b))
+        return statistics.median(ts)
+
+    rows = []
+    for kind, name, moved in ((0, "read", 1), (1, "write", 1), (2, "copy", 2)):
+        for nt in (0, 1):
+            for grid in (1024, 2048, 4096, 8192, 16384):
+                d = None if kind == 0 else dst.data_ptr()
+                ms = timed(lambda: _abi.check(lib.mmuon_hbm_stream(kind, d, src.data_ptr(), nbytes, nt, grid, stream),
+                                              "mmuon_hbm_stream"))
+                rows.append({"kind": name, "nontemporal": nt, "grid": grid, "ms": round(ms, 4),
+                             "gbs": round(moved * nbytes / (ms * 1e-3) / 1e9, 1)})
+    ms = timed(lambda: dst.copy_(src))
+    rows.append({"kind": "copy", "nontemporal": None, "grid": "torch copy_", "ms": round(ms, 4),
+                 "gbs": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)})
+    best = {k: max((r for r in rows if r["kind"] == k), key=lambda r: r["gbs"]) for k in ("read", "write", "copy")}
+    print(json.dumps({"metric": "HBM stream bandwidth (GB/s, read + written)", "bytes": nbytes,
+                      "peak_gbs": PEAK_HBM_GBS, "best": best, "rows": rows}), flush=True)
+
+
+# ---------------------------------------------------------------- power and clock
+class PowerSampler:
+    """Socket power, GFX clock and the energy counter of this GPU (amdsmi),
+    sampled from a thread every few ms."""
+
+    def __init__(self, device):
+        import amdsmi
+        self.smi = amdsmi
+        amdsmi.amdsmi_init()
+        handles = amdsmi.amdsmi_get_processor_handles()
+        if not handles:
+            raise RuntimeError("amdsmi sees no GPU")
+        self.h = handles[0]
+        if len(handles) > 1:
+            bus = torch.cuda.get_device_properties(device).pci_bus_id
+            for h in handles:
+                if int(amdsmi.amdsmi_get_gpu_device_bdf(h).split(":")[1], 16) == bus:
+                    self.h = h
+        self.samples = []
+        self._stop = None
+
+    def energy_j(self):
+        e = self.smi.amdsmi_get_energy_count(self.h)
+        return e["energy_accumulator"] * e["counter_resolution"] * 1e-6
+
+    def _read(self):
+        m = self.smi.amdsmi_get_gpu_metrics_info(self.h)
+
+        def num(x):
+            return x if isinstance(x, (int, float)) else None
+
+        clks = [c for c in (m.get("current_gfxclks") or []) if isinstance(c, (int, float)) and c > 0]
+        clk = sum(clks) / len(clks) if clks else num(m.get("current_gfxclk"))
+        return (time.perf_counter(), num(m.get("current_socket_power")), clk,
+                num(m.get("average_gfxclk_frequency")), num(m.get("throttle_status")))
+
+    def start(self):
+        import threading
+        self.samples = []
+        self._stop = threading.Event()
+
+        def loop():
+            while not self._stop.is_set():
+                try:
+                    self.samples.append(self._read())
+                except Exception:  # a failed read leaves a gap, nothing more
+                    pass
+                time.sleep(0.004)
+
+        self._thread = threading.Thread(target=loop, daemon=True)
+        self._thread.start()
+
+    def stop(self, skip_s=0.3):
+        self._stop.set()
+        self._thread.join()
+        t0 = self.samples[0][0] if self.samples else 0
+        s = [x for x in self.samples if x[0] - t0 >= skip_s]
+
+        def mean(i):
+            v = [x[i] for x in s if x[i] is not None]
+            return round(sum(v) / len(v), 1) if v else None
+        return {"socket_w": mean(1), "gfx_mhz": mean(2), "avg_gfx_mhz": mean(3), "samples": len(s)}
+
+
+def power_profile(args, w):
+    """Each kernel of one optimizer step on the 1024 x 1024 group (and the
+    AdamW group, and the whole step) launched back to back for about two
+    seconds: ms per launch, socket power, GFX clock, and energy per launch
+    from the energy counter."""
+    from monarch_muon_amd import _abi
+    from monarch_muon_amd.optim import _COEFFS
+    from monarch_muon_amd.plan import NS_STEPS
+    dev = torch.device("cuda", 0)
+    muon, adamw, opt = build_gpu(w, dev)
+    opt.step()
+    torch.cuda.synchronize()
+    lib = _abi.lib()
+    gl = opt._muon_planner.groups[0]
+    stream = _abi.stream_handle(dev)
+    sampler = PowerSampler(dev)
+    alpha = -0.02 * gl.alpha_scale
+
+    def stage(it, st):
+        return lambda: _abi.check(lib.mmuon_ns_stage(C.byref(gl.struct), it, NS_STEPS, st, _COEFFS, alpha, 0, stream),
+                                  "mmuon_ns_stage")
+
+    cases = [
+        ("pack_rows_kernel (1024x1024 group)",
+         lambda: _abi.check(lib.mmuon_momentum_pack(C.byref(gl.struct), 0.95, stream), "pack")),
+        ("ns_sym_bf16<0> SYRK (1024x1024 group, iteration 2)", stage(1, 0)),
+        ("ns_sym_bf16<1> POLY (1024x1024 group, iteration 2)", stage(1, 1)),
+        ("ns_px_bf16<2> PX (1024x1024 group, iteration 2)", stage(1, 2)),
+        ("ns_px_bf16<3> PX + apply (1024x1024 group)", stage(NS_STEPS - 1, 2)),
+        ("adamw_kernel (AdamW group)", lambda: opt._adamw_step(opt.param_groups[1], 0.02)),
+        ("full optimizer step", lambda: opt.step()),
+    ]
+    rows = []
+    time.sleep(1.0)
+    sampler.start()
+    time.sleep(1.0)
+    idle = sampler.stop(skip_s=0.2)
+    rows.append({"kernel": "idle (nothing launched)", **idle})
+    for name, fn in cases:
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        one = time.perf_counter() - t0
+        n = max(3, int(args.power_seconds / max(one, 1e-4)))
+        sampler.start()
+        time.sleep(0.05)
+        e0, t0 = sampler.energy_j(), time.perf_counter()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        t1, e1 = time.perf_counter(), sampler.energy_j()
+        st = sampler.stop()
+        ms = a.elapsed_time(b) / n
+        rows.append({"kernel": name, "launches": n, "ms": round(ms, 4), **st,
+                     "energy_j_per_launch": round((e1 - e0) / n, 3),
+                     "energy_w": round((e1 - e0) / (t1 - t0), 1)})
+        log(f"[bench] {name}: {ms:.3f} ms, {st['socket_w']} W, {st['gfx_mhz']} MHz")
+        time.sleep(0.5)
+    print(json.dumps({"metric": "socket power / GFX clock / energy per kernel", "workload": w.name,
+                      "group": f"{gl.rows}x{gl.cols}x{gl.nblocks}", "rows": rows}), flush=True)
+
+
+# ---------------------------------------------------------------- rocprofv3 counter summaries
+def short_kernel_name(name):
+    """``void mmuon::(anonymous namespace)::ns_px_bf16<2, false, mmuon::(anonymous
+    namespace)::BF16T>(mmuon::NsArgs, int)`` -> ``ns_px_bf16<2, false, BF16T>``."""
+    n = name.strip().strip('"')
+    if n.startswith("void "):
+        n = n[5:]
+    depth, cut = 0, len(n)
+    for i, ch in enumerate(n):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0 and not n[i:].startswith("(anonymous"):
+            cut = i
+            break
+    n = n[:cut]
+    for pre in ("mmuon::(anonymous namespace)::", "mmuon::"):
+        n = n.replace(pre, "")
+    return n
+
+
+def counter_summary(paths):
+    """Per-kernel mean of every counter over the dispatches in rocprofv3
+    ``*counter_collection.csv`` files, plus the mean dispatch duration (ns)."""
+    import csv
+    per = defaultdict(lambda: defaultdict(list))
+    dur = defaultdict(dict)
+    for path in paths:
+        with open(path, newline="") as f:
+            vals = defaultdict(float)
+            for r in csv.DictReader(f):
+                k = short_kernel_name(r["Kernel_Name"])
+                key = (path, r["Dispatch_Id"], k)
+                vals[key + (r["Counter_Name"],)] += float(r["Counter_Value"])
+                if "Start_Timestamp" in r and r.get("End_Timestamp"):
+                    dur[k][(path, r["Dispatch_Id"])] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        for (p_, d, k, c), v in vals.items():
+            per[k][c].append(v)
+    out = {}
+    for k, cs in per.items():
+        out[k] = {c: sum(v) / len(v) for c, v in cs.items()}
+        out[k]["dispatches"] = max(len(v) for v in cs.values())
+        if dur[k]:
+            out[k]["duration_ns"] = sum(dur[k].values()) / len(dur[k])
+    return out
+
+
+XCDS = 8  # MI355X: GRBM_GUI_ACTIVE is reported summed over the 8 XCDs' GRBMs
+
+
+def mfma_summary(args):
+    """MFMA utilisation per Newton-Schulz kernel from rocprofv3 counter runs
+    (``--mfma-summary OUT.json CSV...``): executed MFMA FLOP (SQ_INSTS_MFMA x
+    32768, every instruction of these kernels being v_mfma_f32_32x32x16_bf16;
+    SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 where that counter was collected), the
+    GFX clock the counters imply (GRBM_GUI_ACTIVE / 8 XCDs / duration) and the
+    MFMA busy fraction of all 1024 SIMDs' cycles (SQ_VALU_MFMA_BUSY_CYCLES /
+    (GRBM_GUI_ACTIVE / 8 x 1024), rocprofv3's MfmaUtil)."""
+    out_path, *csvs = args.mfma_summary
+    s = counter_summary(csvs)
+    simds = 1024
+    res = {}
+    for k, c in s.items():
+        if not k.startswith("ns_") or "SQ_INSTS_MFMA" not in c or "duration_ns" not in c:
+            continue
+        secs = c["duration_ns"] * 1e-9
+        flop = c["SQ_INSTS_MFMA"] * 32768.0
+        rec = {"dispatches": c["dispatches"], "avg_ms": round(secs * 1e3, 4), "exec_flop": flop,
+               "exec_tflops": round(flop / secs / 1e12, 1),
+               "exec_frac_peak": round(flop / secs / 1e12 / PEAK_BF16_TFLOPS, 4)}
+        if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in c:
+            rec["mops_flop"] = c["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512.0
+        if "GRBM_GUI_ACTIVE" in c:
+            cycles = c["GRBM_GUI_ACTIVE"] / XCDS
+            rec["gfx_mhz"] = round(cycles / secs / 1e6, 1)
+            # what the kernel executed against the peak at the clock it ran at
+            rec["exec_frac_at_clock"] = round(flop / (cycles * simds * 1024.0), 4)
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+                rec["mfma_busy"] = round(c["SQ_VALU_MFMA_BUSY_CYCLES"] / (cycles * simds), 4)
+        res[k] = rec
+    Path(out_path).write_text(json.dumps({"simds": simds, "kernels": res}, indent=1) + "\n")
+    print(json.dumps(res, indent=1))
+
+
+def mfma_util(workload, kernel):
+    """The committed MFMA-counter summary of `kernel` at `workload`, or None."""
+    try:
+        data = json.loads((ROOT / "profiles" / f"mfma_util_{workload}.json").read_text())
+        return data["kernels"][kernel]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 # ---------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser()
@@ -418,7 +776,19 @@ def main():
                          "the fused clip and torch.nn.utils.clip_grad_norm_ on the same gradients")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy (for HBM counter calibration)")
+    ap.add_argument("--fresh-steps", type=int, default=5,
+                    help="steps of the fresh-gradient leg (host planner time); 0 skips it")
+    ap.add_argument("--hbm-ceiling", action="store_true", help="only measure read / write / copy bandwidth")
+    ap.add_argument("--power", action="store_true",
+                    help="only measure socket power, GFX clock and energy per step kernel")
+    ap.add_argument("--power-seconds", type=float, default=2.0)
+    ap.add_argument("--mfma-summary", nargs="+", metavar=("OUT_JSON", "CSV"),
+                    help="summarise rocprofv3 counter CSVs (SQ_INSTS_MFMA, SQ_VALU_MFMA_BUSY_CYCLES, "
+                         "GRBM_GUI_ACTIVE) into OUT_JSON")
     args = ap.parse_args()
+    if args.mfma_summary:
+        mfma_summary(args)
+        return
     if args.copy_calibration:
         x = torch.ones(2 ** 28, dtype=torch.float32, device="cuda")
         y = torch.empty_like(x)
@@ -432,6 +802,12 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     from monarch_muon_amd.workloads import WORKLOADS, adamw_elements, muon_elements, ns_flops
+    if args.hbm_ceiling:
+        hbm_ceiling(args)
+        return
+    if args.power:
+        power_profile(args, WORKLOADS[args.workload])
+        return
     if args.workload.startswith("butterfly-"):
         model = args.workload[len("butterfly-"):]
         base = next(k for k in WORKLOADS if k.split("-")[0] == model)
@@ -484,6 +860,7 @@ def main():
     d_avg = d_ms / d_n
     achieved = (d_fl / d_n) / (d_avg * 1e-3) / 1e12
     traffic = hbm_traffic(w.name, dominant)
+    counters = mfma_util(w.name, dominant)
     kernels = {k: {"avg_ms": round(v[0] / v[1], 4), "launches_per_step": v[1] // reps,
                    "ms_per_step": round(v[0] / reps, 3),
                    **({"alg_tflops": round(v[2] / (v[0] * 1e-3) / 1e12, 1),
@@ -505,10 +882,19 @@ def main():
                    "newton_schulz": "bf16 MFMA, fp32 accumulate, 5 iterations",
                    "groups": [f"{gl.rows}x{gl.cols}x{gl.nblocks}" for gl in opt._muon_planner.groups]},
         "median_event_ms": round(median_ms, 3),
+        "statistics": {"value": "wall-clock mean of the K timed steps between two device synchronisations",
+                       "median_event_ms": "median of per-step hipEvent pairs, the reference harness's statistic "
+                                          "(benchmark_train_step.py:297-299,386-397: 3 warm-ups, median of 12 "
+                                          "event-timed steps; this script's defaults)"},
         "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic, "avg_launch_ms": round(d_avg, 4),
-                     "alg_flops_per_launch": d_fl / d_n, "exec_tflops": round((d_ex / d_n) / (d_avg * 1e-3) / 1e12, 1)},
+                     "alg_flops_per_launch": d_fl / d_n, "exec_tflops": round((d_ex / d_n) / (d_avg * 1e-3) / 1e12, 1),
+                     **({"exec_frac": round((d_ex / d_n) / (d_avg * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                         "counters": {"source": f"profiles/mfma_util_{w.name}.json",
+                                      **{k: counters[k] for k in ("exec_frac_peak", "exec_frac_at_clock",
+                                                                  "mfma_busy", "gfx_mhz") if k in counters}}}
+                        if counters else {})},
         "newton_schulz": {"ms": round(ns_ms, 3), "alg_tflop": round(ns_flops(w) / 1e12, 2),
                           "alg_tflops": round(ns_tf, 1), "frac_peak": round(ns_tf / PEAK_BF16_TFLOPS, 4)},
         "momentum_pack": {"ms": round(pack_ms, 3), "alg_bytes": pack_b,
@@ -520,6 +906,10 @@ def main():
         "kernels": kernels,
         "reference_h100_ms": REFERENCE_H100_MS,
     }
+    if w.momentum_dtype == torch.bfloat16 and w.name.startswith("6.89b"):
+        # the states the published H100 step time was measured with (bf16 params, grads, momentum)
+        res["vs_baseline"] = round(wall_ms / REFERENCE_H100_MS, 4)
+        res["vs_baseline_note"] = "value / 304.4 ms (README.md:16, 1x H100, bf16 momentum); lower is faster"
     if args.grad_clip:
         params = muon + adamw
 
@@ -539,6 +929,10 @@ def main():
         res["grad_clip"] = {"max_norm": args.grad_clip, "fused_clip_ms": round(fused, 3),
                             "torch_clip_grad_norm_ms": round(ref, 3),
                             "note": "value/ms_per_step include opt.clip_grad_norm_ before every step"}
+    if args.fresh_steps > 0:
+        log(f"[bench] fresh-gradient leg ({args.fresh_steps} steps)")
+        res["fresh_grads"] = fresh_grad_leg(opt, muon + adamw, args.fresh_steps)
+        res["host_plan_ms"] = res["fresh_grads"]["host_plan_ms"]
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle on host cores, bounded sample)")
         res["cpu_baseline"] = cpu_baseline(w)

@@ -137,7 +137,11 @@ int mmuon_newton_schulz_apply(const mmuon_group* g, int32_t iters, const float c
 
 /* One stage of one Newton-Schulz iteration (stage 0 = Gram X X^T, 1 = polynomial,
    2 = X update; on the last iteration stage 2 also applies the weight update
-   unless MMUON_NS_NO_APPLY).  mmuon_newton_schulz_apply is exactly the loop
+   unless MMUON_NS_NO_APPLY).  With a bf16 group the polynomial stage stores
+   P = a I + b A + c A A (the a X term rides on P's diagonal, added in fp32
+   before P's bf16 rounding) and stage 2 computes X = P X; with an fp32 group it
+   stores P = b A + c A A and stage 2 computes X = a X + P X.
+   mmuon_newton_schulz_apply is exactly the loop
    over (iteration, stage); this entry exists so a caller can time each kernel
    with its own events.  Same reference lines as mmuon_newton_schulz_apply. */
 int mmuon_ns_stage(const mmuon_group* g, int32_t iteration, int32_t iters, int32_t stage,
@@ -293,6 +297,16 @@ int mmuon_butterfly_fwd(const mmuon_butterfly_args* a, void* stream);
 int mmuon_butterfly_bwd(const mmuon_butterfly_args* a, void* stream);
 /* Workspace bytes the backward needs for these shapes (x, pointers unused). */
 size_t mmuon_butterfly_workspace(const mmuon_butterfly_args* a);
+
+/* HBM streaming probe: reads (kind 0: src), writes (kind 1: dst, hashed
+   random-looking data) or copies (kind 2: src -> dst) `bytes` with 16-B vector
+   accesses, grid x 256 threads, grid-stride; nontemporal != 0 uses
+   non-temporal loads and stores.  No counterpart in the reference: it measures
+   the bandwidth this GPU sustains, the ceiling of the step's HBM-bound kernels
+   (momentum pack, AdamW).  bytes a positive multiple of 16, buffers 16-B
+   aligned; kind 0 may pass dst = NULL (else dst holds grid * 4096 bytes). */
+int mmuon_hbm_stream(int32_t kind, void* dst, const void* src, int64_t bytes, int32_t nontemporal,
+                     int32_t grid, void* stream);
 
 /* Thread-local message of the last failing call ("" if none). */
 const char* mmuon_last_error(void);

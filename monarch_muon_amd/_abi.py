@@ -16,7 +16,7 @@ LIB_PATH = Path(os.environ.get("MMUON_LIB", Path(__file__).resolve().parent / "l
 F32, BF16, F8E4M3 = 0, 1, 2
 GROUP_ALIGNED16 = 1
 NS_NO_APPLY = 1
-ABI_VERSION = 4
+ABI_VERSION = 5
 NOALLOC_SCRATCH_FLOATS = 1 << 20
 
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8E4M3}
@@ -114,6 +114,8 @@ SIGNATURES = {
     "mmuon_butterfly_fwd": (C.c_int, [C.POINTER(ButterflyArgs), C.c_void_p]),
     "mmuon_butterfly_bwd": (C.c_int, [C.POINTER(ButterflyArgs), C.c_void_p]),
     "mmuon_butterfly_workspace": (C.c_size_t, [C.POINTER(ButterflyArgs)]),
+    "mmuon_hbm_stream": (C.c_int, [C.c_int32, C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_int32,
+                                   C.c_void_p]),
 }
 
 _lib = None

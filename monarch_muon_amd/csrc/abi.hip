@@ -129,7 +129,7 @@ extern "C" {
 
 const char* mmuon_last_error(void) { return g_err.c_str(); }
 
-int mmuon_abi_version(void) { return 4; }
+int mmuon_abi_version(void) { return 5; }
 
 int mmuon_ns_layout(int32_t rows, int32_t cols, int32_t ns_dtype, int64_t nblocks,
                     mmuon_ns_layout_t* out) {

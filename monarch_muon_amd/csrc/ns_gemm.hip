@@ -2,13 +2,15 @@
 //
 // One Newton-Schulz iteration over a stack of N blocks X (m x n, m <= n):
 //   SYRK : A = s^2 * X X^T                      (m x m, symmetric, K = n)
-//   POLY : P = b A + c A A                      (m x m, symmetric, K = m)
-//   PX   : X' = s * (a X + P X)                 (m x n, K = m)
+//   POLY : P = a I + b A + c A A                (m x m, symmetric, K = m)
+//   PX   : X' = s * P X                         (m x n, K = m)
 //   PX_APPLY (last iteration): param += alpha * bf16(X') written straight into
 //          the parameter blocks, un-transposed for tall blocks.
 // s = 1/(||X0||_F + 1e-7) on the first iteration (the Frobenius normalisation
-// folded into the products: (sX)(sX)^T = s^2 XX^T and a(sX) + P(sX) = s(aX + PX)),
-// 1 afterwards.
+// folded into the products: (sX)(sX)^T = s^2 XX^T and P(sX) = s PX), 1
+// afterwards.  The a X term of the quintic is carried by P's diagonal: POLY adds
+// a to its fp32 diagonal before the one bf16 rounding of P (the reference rounds
+// a X to bf16 in the same way), so PX is a plain product.
 //
 // bf16 kernels: v_mfma_f32_32x32x16_bf16, fp32 accumulation, bf16 stage outputs.
 // One 512-thread workgroup (8 waves, 2 per SIMD) per CU computes 256 x 256
@@ -56,12 +58,11 @@ __device__ __forceinline__ void sym_tile(int t, int nc, int& ti, int& tc) {
 // K slices left of its diagonal block (from the stored tile (kb, R)) and K from
 // there on.  A slice pair (row operand, column operand) is KK, KT or TT.
 // ---------------------------------------------------------------------------
-// Identity terms folded into the accumulation: IDENT_ROW adds v X (X: the
-// column operand) over the K slices that cross the tile's diagonal rows,
-// IDENT_COL adds v A (A: the row operand) over those that cross its diagonal
-// columns.  The values are taken from the slice in LDS and enter the fp32
-// accumulators by FMA (Pipe::ident_add).
-enum { IDENT_NONE = 0, IDENT_ROW = 1, IDENT_COL = 2 };
+// Identity term folded into the accumulation: IDENT_COL adds v A (A: the row
+// operand) over the K slices that cross the tile's diagonal columns.  The
+// values are taken from the slice in LDS and enter the fp32 accumulators by
+// FMA (Pipe::ident_add).
+enum { IDENT_NONE = 0, IDENT_COL = 2 };
 
 enum { OP_K = 0, OP_T = 1, OP_SPLIT = 2 };  // operand form over K: always K, always T, T then K
 enum { M_KK = 0, M_KT = 1, M_TT = 2 };        // forms of one slice pair (row, column)
@@ -104,7 +105,7 @@ struct Pipe {
   uint32_t k_loff;                // per-lane direct-load byte offset of the K form (T form: 16 * lane)
   uint32_t kfrag[BK / 16];        // per-lane K-form fragment bases
   uint32_t tfrag_r, tfrag_c;      // per-lane T-form fragment bases of the wave's first row / column tile
-  int diag0;                      // K index of this wave's first identity row / column
+  int diag0;                      // K index of this wave's first identity column
   float id_v;                     // identity scalar
 
   __device__ __forceinline__ uint16_t* rslot(int kt) const { return lds + (uint32_t(kt) % NSTAGE) * SLOT; }
@@ -172,34 +173,20 @@ struct Pipe {
     if constexpr (frag_on(5)) load_one<KK, 5, M>(kt, f);
   }
 
-  // Identity term of slice kt, which crosses this wave's identity at tile F.
-  // The accumulator of a 32 x 32 tile holds, in lane l, column l%32 and rows
-  // 8q + 4(l/32) + e (value 4q + e); ds_read_b64_tr_b16 gives lane l of a
-  // 16-lane group the four values of one column in four consecutive rows, so
-  // one read per q delivers the lane's four rows.
-  //   IDENT_ROW: acc[F][j] += v X[k][c], k = the accumulator row (the slice's
-  //     row k%32), c its column; X slice in T form, byte p*2048 + k*64 + c*2.
-  //   IDENT_COL: acc[i][F] += v A[r][k], k = the accumulator column; A slice
-  //     in K form, byte r*64 + ((k/8) ^ ((r/4)%4))*16 + (k%8)*2, the same
-  //     chunk order for the four rows r of a read.
+  // Identity term of slice kt, which crosses this wave's identity at tile F:
+  // acc[i][F] += v A[r][k], k = the accumulator column, from the A slice in K
+  // form (byte r*64 + ((k/8) ^ ((r/4)%4))*16 + (k%8)*2, the same chunk order
+  // for the four rows r of a read).  The accumulator of a 32 x 32 tile holds,
+  // in lane l, column l%32 and rows 8q + 4(l/32) + e (value 4q + e);
+  // ds_read_b64_tr_b16 gives lane l of a 16-lane group the four values of one
+  // column in four consecutive rows, so one read per q delivers the lane's
+  // four rows.
   template <int F>
   __device__ __forceinline__ void ident_add(int kt, f32x16 (&acc)[TMI][TMJ]) const {
+    static_assert(IDENT == IDENT_COL, "the column identity is the only one");
     const int l16 = lane & 15, g = lane >> 4;
     const int k16 = 16 * (g & 1) + 4 * (l16 & 3);  // first column of the lane's 8-byte chunk
-    if constexpr (IDENT == IDENT_ROW) {
-      const char* sc = reinterpret_cast<const char*>(rslot(kt) + (SHARED ? 0 : RSLICE));
-      const uint32_t base = uint32_t((4 * (g >> 1) + (l16 >> 2)) * 64 + k16 * 2);
-#pragma unroll
-      for (int j = 0; j < TMJ; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (!tile_on(F, j)) continue;
-          const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_i16x4*)(sc + (wn * TMJ + j) * 2048 + q * 8 * 64 + base));
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[F][j][4 * q + e] = fmaf(id_v, bf2f(uint16_t(v[e])), acc[F][j][4 * q + e]);
-        }
-    } else {
+    {
       const char* sr = reinterpret_cast<const char*>(rslot(kt));
 #pragma unroll
       for (int i = 0; i < TMI; ++i)
@@ -312,16 +299,12 @@ struct Pipe {
       // the slices starting at diag0 cross this wave's identity tiles in
       // order (diag0 is a multiple of the wave's extent along K and lies in
       // the last run)
-      constexpr int NI = IDENT == IDENT_ROW ? TMI : TMJ;
+      static_assert(TMJ == 2, "a wave's identity columns span two slices");
       const int kd = diag0 / BK;
       for (int kt = k0; kt < kd; ++kt) body<ML, ML, -1, ML>(kt, fa, fb, acc);
       body<ML, ML, 0, ML>(kd, fa, fb, acc);
       body<ML, ML, 1, ML>(kd + 1, fa, fb, acc);
-      if constexpr (NI == 4) {
-        body<ML, ML, 2, ML>(kd + 2, fa, fb, acc);
-        body<ML, ML, 3, ML>(kd + 3, fa, fb, acc);
-      }
-      for (int kt = kd + NI; kt < KT; ++kt) body<ML, ML, -1, ML>(kt, fa, fb, acc);
+      for (int kt = kd + TMJ; kt < KT; ++kt) body<ML, ML, -1, ML>(kt, fa, fb, acc);
     }
     wait_vm<0>();  // the refills of the last two steps land before the ring is reused
   }
@@ -396,7 +379,7 @@ __device__ __forceinline__ void mainloop_run(const uint16_t* rsrc_k, const uint1
   for (int kk = 0; kk < BK / 16; ++kk) p.kfrag[kk] = kmajor_frag_base(kk, p.lane);
   p.tfrag_r = rowmajor_frag_base(p.wm * TMI, p.lane);
   p.tfrag_c = rowmajor_frag_base(p.wn * TMJ, p.lane);
-  p.diag0 = diag + (IDENT == IDENT_ROW ? p.wm * WM : p.wn * WN);
+  p.diag0 = diag + p.wn * WN;
   p.id_v = ident_v;
   p.run(acc);
 }
@@ -404,7 +387,7 @@ __device__ __forceinline__ void mainloop_run(const uint16_t* rsrc_k, const uint1
 // Operand sources: *_k the K form (panel 0 at the operand's first row), *_t the
 // T form (row 0 of the first panel holding the operand's rows); thr_*: slices
 // kt < thr are T (OP_SPLIT); pstride: elements per panel.  ident_v: the identity
-// scalar; diag: K index of the tile's first row (IDENT_ROW) or column (IDENT_COL).
+// scalar; diag: K index of the tile's first column (IDENT_COL).
 // sym_diag (workgroup-uniform): a diagonal tile of a symmetric product, whose
 // row and column operands are the same rows (loaded once, Pipe SHARED) and
 // whose work is dealt by diag_plan.  idle (wave-uniform, full tiles only): the
@@ -435,9 +418,10 @@ __device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t*
 // j = 64 wn + 32 tj + lane%32 and rows i = 128 wm + 32 ti + 8 qg + 4 (lane/32) + e,
 // (wm, wn) the wave's window.  diag: a diagonal tile of a symmetric product
 // computed by diag_plan; every computed tile above the diagonal also fills its
-// mirror below it, T[i][j] = D[i][j].
+// mirror below it, T[i][j] = D[i][j]; and its diagonal entries i = j < dlim get
+// dadd added (in fp32, before the rounding).
 __device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI][TMJ], float f,
-                                           bool diag = false) {
+                                           bool diag = false, float dadd = 0.f, int dlim = 0) {
   const int tid = fresh_tid();
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const WavePlan plan = diag ? diag_plan(wave) : full_plan(wave);
@@ -453,6 +437,16 @@ __device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI]
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = f * acc[i][j][qg * 4 + e];
+        if (diag && R == C) {
+          // the 32 x 32 tile on the diagonal: lane l holds entry (l%32, l%32)
+          // at qg = (l%32)/8, e = l%8 - 4 (l/32) when that lies in [0, 4)
+          const int d = lane & 31, e = (d & 7) - 4 * (lane >> 5);
+          if ((d >> 3) == qg && e >= 0 && e < 4 && 32 * R + d < dlim) {
+#pragma unroll
+            for (int x = 0; x < 4; ++x)
+              if (x == e) v[x] += dadd;
+          }
+        }
         const int row = wn * WN + j * 32 + (lane & 31);
         const int col = wm * WM + i * 32 + qg * 8 + (lane >> 5) * 4;
         *reinterpret_cast<uint2*>(stage + tile_off(row, col)) = make_uint2(f2bf2(v[0], v[1]), f2bf2(v[2], v[3]));
@@ -551,7 +545,7 @@ __device__ __forceinline__ void sym_work(const NsArgs& a, uint16_t* lds, int v) 
   if (STAGE == NS_SYRK)
     mainloop<OP_K, OP_K>(src + r0 * PANEL, nullptr, 0, src + c0 * PANEL, nullptr, 0, pstride, K / BK, lds, acc,
                          0.f, 0, diag);
-  else  // acc = A A + (b/c) A, so P = c acc = b A + c A A
+  else  // acc = A A + (b/c) A, so P = c acc + a I = a I + b A + c A A
     mainloop<OP_SPLIT, OP_SPLIT, IDENT_COL>(src + r0 * PANEL, src + (r0 / PANEL) * pstride, r0 / BK,
                                             src + c0 * PANEL, src + (c0 / PANEL) * pstride, c0 / BK,
                                             pstride, K / BK, lds, acc, a.cb / a.cc, c0, diag);
@@ -564,7 +558,8 @@ __device__ __forceinline__ void sym_work(const NsArgs& a, uint16_t* lds, int v) 
   uint16_t* out = static_cast<uint16_t*>(a.out) + int64_t(b) * a.mp * a.mp;
   char* stage = reinterpret_cast<char*>(lds);
   barrier();  // every wave is done with the ring
-  stage_tile(stage, acc, f, diag);
+  // POLY: a on the diagonal of the m valid rows (the padding stays zero)
+  stage_tile(stage, acc, f, diag, STAGE == NS_POLY ? a.ca : 0.f, STAGE == NS_POLY ? a.m - r0 : 0);
   barrier();
   if (!diag) {
     // upper tile C[r0 + i][c0 + r] = T[r][i]
@@ -588,9 +583,9 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void ns_sym_bf16(NsArgs a, int total
 }
 
 // ---------------------------------------------------------------------------
-// PX / PX_APPLY: X' = s (a X + P X), m x n output tile (256 x 256), K = m.
-// D[i][j] in registers (lane holds column j, rows i..i+3); the a X term enters
-// the accumulation as (a I) X.  T[j][i] = X'[r0 + i][c0 + j] is staged in LDS;
+// PX / PX_APPLY: X' = s P X (P = a I + b A + c A A from POLY), m x n output
+// tile (256 x 256), K = m.  D[i][j] in registers (lane holds column j, rows
+// i..i+3).  T[j][i] = X'[r0 + i][c0 + j] is staged in LDS;
 // X' rows (PX, and the parameter rows of an untransposed block) are T's
 // columns, the parameter rows of a tall block (param[j][i]) are T's rows.
 // ---------------------------------------------------------------------------
@@ -634,23 +629,29 @@ __device__ __forceinline__ void apply_chunk(typename TP::storage* prm, int64_t o
 
 template <int STAGE, bool TRANS, class TP>
 __device__ __forceinline__ void px_work(const NsArgs& a, uint16_t* lds, int v) {
-  const int tiles_j = a.np / BN;
-  const int tiles = (a.mp / BM) * tiles_j;
+  const int tiles_i = a.mp / BM;
+  const int tiles = tiles_i * (a.np / BN);
   int b, t;
   if (!decode_tile(v, tiles, a.N, b, t)) return;
-  const int ti = t / tiles_j, tc = t % tiles_j;
+  // column-band-major: the tiles_i tiles that read one column band of X are
+  // consecutive virtual tiles, so they run in the same round on one XCD
+  // whenever tiles_i divides the workgroups one XCD runs per round (32 on 256
+  // CUs; m <= 1024 at every model size here) and the band is fetched from HBM
+  // once.  A block with more tiles than a round (n = 2752: 44) is split
+  // between rounds at a column-band boundary, so only its P row bands, the
+  // smaller operand, are fetched twice.
+  const int tc = t / tiles_i, ti = t % tiles_i;
   const int r0 = ti * BM, c0 = tc * BN;
 
   const int64_t pstride = int64_t(a.mp) * PANEL;
   const uint16_t* P = static_cast<const uint16_t*>(a.a_in) + int64_t(b) * a.mp * a.mp;
   const uint16_t* X = static_cast<const uint16_t*>(a.x_in) + int64_t(b) * a.mp * a.np + (c0 / PANEL) * pstride;
   f32x16 acc[TMI][TMJ];
-  // acc = P X + a X (the a X term added from the X slices of the tile's diagonal
-  // rows); a wave whose 64 columns all lie in the zero padding (n <= column <
-  // np) computes nothing: its part of X' stays zero
+  // acc = P X; a wave whose 64 columns all lie in the zero padding (n <= column
+  // < np) computes nothing: its part of X' stays zero
   const int wn = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) % NWN;
-  mainloop<OP_SPLIT, OP_T, IDENT_ROW>(P + r0 * PANEL, P + (r0 / PANEL) * pstride, r0 / BK, nullptr, X, 0,
-                                      pstride, a.mp / BK, lds, acc, a.ca, r0, false, c0 + wn * WN >= a.n);
+  mainloop<OP_SPLIT, OP_T>(P + r0 * PANEL, P + (r0 / PANEL) * pstride, r0 / BK, nullptr, X, 0, pstride, a.mp / BK,
+                           lds, acc, 0.f, 0, false, c0 + wn * WN >= a.n);
 
   const float s = a.scale != nullptr ? a.scale[b] : 1.f;
   char* stage = reinterpret_cast<char*>(lds);

@@ -38,6 +38,10 @@ WORKLOADS = {
     "6.89b-nb4": Workload("6.89b-nb4", 32, 4096, 32, 11008, 4, torch.bfloat16, torch.float32, torch.bfloat16, True),
     # FP8 e4m3 momentum (group 128), bf16 Newton-Schulz
     "6.89b-nb4-fp8": Workload("6.89b-nb4-fp8", 32, 4096, 32, 11008, 4, torch.bfloat16, "fp8", torch.bfloat16, True),
+    # the optimizer states the reference's published step time was measured with: bf16 params, grads and
+    # momentum (membench/scripts/monarch_benchmark/benchmark_train_step.py:428-436 asserts bf16 states)
+    "6.89b-nb4-bf16mom": Workload("6.89b-nb4-bf16mom", 32, 4096, 32, 11008, 4, torch.bfloat16, torch.bfloat16,
+                                  torch.bfloat16, True),
 }
 
 

@@ -179,23 +179,40 @@ def _build(w, draws, device, opt_cls, **kw):
 
 
 @pytest.mark.parametrize("name,layers,rows", [("toy", None, None), ("257m-nb2", 2, 512), ("1.3b-nb4", 1, 256),
-                                              ("6.89b-nb4", 1, 256)])
+                                              ("6.89b-nb4", 1, 256), ("6.89b-nb4-bf16mom", 1, 256)])
 def test_workload_step_matches_oracle(name, layers, rows):
     w, draws = _workload_params(name, layers, rows)
     gm, ga, gopt, _ = _build(w, draws, DEV, MonarchMuonOptimizer, ns_dtype=w.ns_dtype)
     variant = "membench" if w.ns_dtype == torch.bfloat16 else "pretrain"
     cm, ca, copt, _ = _build(w, draws, "cpu", ReferenceMonarchMuon, variant=variant)
+    # bf16 momentum: the update as torch's GPU kernels execute the reference's
+    # foreach ops (buf *= mu; buf += g; mu kept in fp32), bit for bit
+    gpu_mom = None
+    if w.momentum_dtype == torch.bfloat16:
+        gpu_mom = [(B.to(torch.bfloat16).to(DEV), G.to(torch.bfloat16).to(DEV)) for _, m, _, G, B in draws if m]
     for _ in range(2):
         gopt.step()
         copt.step()
+        if gpu_mom is not None:
+            bufs = [b for b, _ in gpu_mom]
+            torch._foreach_mul_(bufs, 0.95)
+            torch._foreach_add_(bufs, [g for _, g in gpu_mom])
     torch.cuda.synchronize()
     tol = BF16_TOL if variant == "membench" else F32_TOL
     worst = 0.0
-    for p, q in zip(gm, cm):
+    for i, (p, q) in enumerate(zip(gm, cm)):
         e = blocks_rel(p, q).max().item()
         worst = max(worst, e)
         assert e <= tol
-        assert torch.equal(gopt.state[p]["momentum_buffer"].cpu(), copt.state[q]["momentum_buffer"])
+        ours, ref = gopt.state[p]["momentum_buffer"], copt.state[q]["momentum_buffer"]
+        if gpu_mom is None:
+            assert torch.equal(ours.cpu(), ref)
+        else:
+            assert torch.equal(ours, gpu_mom[i][0])
+            # torch's CPU kernels round mu to bf16 first (0.9492 for 0.95), which
+            # moves entries where mu*buf and g nearly cancel by many bf16 steps;
+            # against the CPU oracle the bar is the north star's per-block one
+            assert blocks_rel(ours, ref).max() <= BF16_TOL
     for p, q in zip(ga, ca):
         assert blocks_rel(p, q).max() <= tol
     print(f"{name}: worst per-block weight error {worst:.3e} (bar {tol})")

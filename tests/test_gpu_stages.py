@@ -5,8 +5,9 @@ inputs as the library left them in the workspace, so a stage is checked in
 isolation (the end-to-end chain is covered in test_gpu_parity.py):
 
   SYRK  A  = s^2 X X^T          (tiles on and above the diagonal are stored)
-  POLY  P  = b A + c A A        (A's lower tiles are the transposes of its upper ones)
-  PX    X' = s (a X + P X)
+  POLY  P  = a I + b A + c A A  (A's lower tiles are the transposes of its upper ones;
+                                 a only on the diagonal of the m valid rows)
+  PX    X' = s P X
 
 Bar: |stage - fp64| <= 2^-8 * max|fp64| per block (one bf16 step at the largest
 entry; bf16 output rounding is at most half of that).  Diagonal 256 x 256 tiles
@@ -88,11 +89,15 @@ def test_stage_outputs_against_fp64_products(shape):
     stage(0, 1)  # POLY from the stored A
     full_a = mirror_upper(a)
     pm = panels(ws.p, nb, mp, mp)
-    check_upper_tiles(pm, b_c * full_a + c_c * (full_a @ full_a), "POLY")
+    eye = torch.zeros(mp, mp, dtype=torch.float64)
+    eye[range(lay.m), range(lay.m)] = 1.0
+    check_upper_tiles(pm, a_c * eye + b_c * full_a + c_c * (full_a @ full_a), "POLY")
+    # the padding rows and columns of P stay zero, its diagonal included
+    assert float(pm[:, lay.m:, :].abs().max() if lay.m < mp else 0.0) == 0.0
 
     stage(0, 2)  # PX from the stored P and X (first iteration: scaled by s)
     full_p = mirror_upper(pm)
-    ref = s * (a_c * x + full_p @ x)
+    ref = s * (full_p @ x)
     got = panels(ws.x1, nb, mp, np_)
     for b in range(nb):
         bound = 2.0 ** -8 * float(ref[b].abs().max())
