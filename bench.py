@@ -561,6 +561,24 @@ class PowerSampler:
         e = self.smi.amdsmi_get_energy_count(self.h)
         return e["energy_accumulator"] * e["counter_resolution"] * 1e-6
 
+    VIOLATIONS = ("acc_counter", "acc_ppt_pwr", "acc_socket_thrm", "acc_vr_thrm", "acc_hbm_thrm", "acc_prochot_thrm")
+
+    def violations(self):
+        """Firmware throttle accumulators: acc_counter ticks, and the ticks during
+        which each limiter held the clock (package power, socket / VR / HBM
+        temperature, PROCHOT)."""
+        try:
+            v = self.smi.amdsmi_get_violation_status(self.h)
+            return {k: v[k] for k in self.VIOLATIONS if isinstance(v.get(k), int)}
+        except Exception:  # older firmware: no violation counters
+            return {}
+
+    def power_cap_w(self):
+        try:
+            return self.smi.amdsmi_get_power_cap_info(self.h)["power_cap"] / 1e6
+        except Exception:
+            return None
+
     def _read(self):
         m = self.smi.amdsmi_get_gpu_metrics_info(self.h)
 
@@ -617,6 +635,16 @@ def power_profile(args, w):
     stream = _abi.stream_handle(dev)
     sampler = PowerSampler(dev)
     alpha = -0.02 * gl.alpha_scale
+    # the vendor library (hipBLASLt through torch) on the same batched shape as the
+    # PX launch of this group, and on one large square product, under the same limits
+    g = torch.Generator(device=dev).manual_seed(1)
+    bm = min(gl.nblocks, 1408)
+    A = torch.randn(bm, 1024, 1024, device=dev, generator=g).bfloat16()
+    B = torch.randn(bm, 1024, 1024, device=dev, generator=g).bfloat16()
+    Cb = torch.empty_like(A)
+    X8 = torch.randn(8192, 8192, device=dev, generator=g).bfloat16()
+    Y8 = torch.randn(8192, 8192, device=dev, generator=g).bfloat16()
+    Z8 = torch.empty_like(X8)
 
     def stage(it, st):
         return lambda: _abi.check(lib.mmuon_ns_stage(C.byref(gl.struct), it, NS_STEPS, st, _COEFFS, alpha, 0, stream),
@@ -631,7 +659,12 @@ def power_profile(args, w):
         ("ns_px_bf16<3> PX + apply (1024x1024 group)", stage(NS_STEPS - 1, 2)),
         ("adamw_kernel (AdamW group)", lambda: opt._adamw_step(opt.param_groups[1], 0.02)),
         ("full optimizer step", lambda: opt.step()),
+        (f"torch.bmm bf16 {bm} x 1024^3 (hipBLASLt, PX's shape)", lambda: torch.bmm(A, B, out=Cb)),
+        ("torch.mm bf16 8192^3 (hipBLASLt)", lambda: torch.mm(X8, Y8, out=Z8)),
     ]
+    flops = {cases[1][0]: stage_exec_flops("syrk", gl), cases[2][0]: stage_exec_flops("poly", gl),
+             cases[3][0]: stage_exec_flops("px", gl), cases[4][0]: stage_exec_flops("px", gl),
+             cases[7][0]: 2.0 * bm * 1024 ** 3, cases[8][0]: 2.0 * 8192 ** 3}
     rows = []
     time.sleep(1.0)
     sampler.start()
@@ -648,6 +681,7 @@ def power_profile(args, w):
         n = max(3, int(args.power_seconds / max(one, 1e-4)))
         sampler.start()
         time.sleep(0.05)
+        v0 = sampler.violations()
         e0, t0 = sampler.energy_j(), time.perf_counter()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
@@ -656,15 +690,23 @@ def power_profile(args, w):
         b.record()
         torch.cuda.synchronize()
         t1, e1 = time.perf_counter(), sampler.energy_j()
+        v1 = sampler.violations()
         st = sampler.stop()
         ms = a.elapsed_time(b) / n
-        rows.append({"kernel": name, "launches": n, "ms": round(ms, 4), **st,
-                     "energy_j_per_launch": round((e1 - e0) / n, 3),
-                     "energy_w": round((e1 - e0) / (t1 - t0), 1)})
+        row = {"kernel": name, "launches": n, "ms": round(ms, 4), **st,
+               "energy_j_per_launch": round((e1 - e0) / n, 3), "energy_w": round((e1 - e0) / (t1 - t0), 1)}
+        ticks = v1.get("acc_counter", 0) - v0.get("acc_counter", 0)
+        if ticks > 0:
+            row["limited_frac"] = {k[4:]: round((v1[k] - v0[k]) / ticks, 3) for k in v0
+                                   if k != "acc_counter" and k in v1}
+        if name in flops:
+            row["exec_tflops"] = round(flops[name] / (ms * 1e-3) / 1e12, 1)
+        rows.append(row)
         log(f"[bench] {name}: {ms:.3f} ms, {st['socket_w']} W, {st['gfx_mhz']} MHz")
         time.sleep(0.5)
     print(json.dumps({"metric": "socket power / GFX clock / energy per kernel", "workload": w.name,
-                      "group": f"{gl.rows}x{gl.cols}x{gl.nblocks}", "rows": rows}), flush=True)
+                      "group": f"{gl.rows}x{gl.cols}x{gl.nblocks}", "power_cap_w": sampler.power_cap_w(),
+                      "rows": rows}), flush=True)
 
 
 # ---------------------------------------------------------------- rocprofv3 counter summaries
@@ -713,6 +755,57 @@ def counter_summary(paths):
         if dur[k]:
             out[k]["duration_ns"] = sum(dur[k].values()) / len(dur[k])
     return out
+
+
+def traffic_summary(args):
+    """HBM bytes per dispatch from rocprofv3 counter runs of this script
+    (``--traffic-summary OUT.json FETCH_CSV WRITE_CSV CAL_FETCH_CSV CAL_WRITE_CSV``):
+    FETCH_SIZE and WRITE_SIZE (KiB) of every kernel, each scaled by what the same
+    counter reads for ``--copy-calibration``'s 1 GiB copy; per kernel the mean
+    over its dispatches, and for the Newton-Schulz and pack kernels of the last
+    (instrumented) step of a 6.89B run, the value of every group and iteration
+    (the instrumented step launches, per group in plan order, the pack, then
+    SYRK, POLY, PX for each iteration)."""
+    out_path, fetch_csv, write_csv, cal_f, cal_w = args.traffic_summary
+    cf, cw = counter_summary([cal_f]), counter_summary([cal_w])
+    copy = next(k for k in cf if "copyBuffer" in k or "copy" in k.lower())
+    copy_bytes = 1 << 30
+    fscale = copy_bytes / (cf[copy]["FETCH_SIZE"] * 1024)
+    wscale = copy_bytes / (cw[copy]["WRITE_SIZE"] * 1024)
+    f, wr = counter_summary([fetch_csv]), counter_summary([write_csv])
+    kernels = {}
+    for k in f:
+        if k in wr and (k.startswith(("ns_", "pack", "adamw", "fp8_")) or "butterfly" in k):
+            b = f[k]["FETCH_SIZE"] * 1024 * fscale + wr[k]["WRITE_SIZE"] * 1024 * wscale
+            kernels[k] = {"fetch_kib": f[k]["FETCH_SIZE"], "write_kib": wr[k]["WRITE_SIZE"], "bytes": b,
+                          "read_bytes": f[k]["FETCH_SIZE"] * 1024 * fscale,
+                          "write_bytes": wr[k]["WRITE_SIZE"] * 1024 * wscale, "dispatches": f[k]["dispatches"]}
+
+    def seq(path, counter):
+        import csv
+        rows = {}
+        with open(path, newline="") as fh:
+            for r in csv.DictReader(fh):
+                k = short_kernel_name(r["Kernel_Name"])
+                if k.startswith(("ns_", "pack")) and r["Counter_Name"] == counter:
+                    d = rows.setdefault(int(r["Dispatch_Id"]), [k, 0.0])
+                    d[1] += float(r["Counter_Value"])
+        return [rows[i] for i in sorted(rows)]
+
+    fs, ws_ = seq(fetch_csv, "FETCH_SIZE"), seq(write_csv, "WRITE_SIZE")
+    groups = [("1024x1024", 1408, 1024, 1024), ("2752x1024", 256, 1024, 2752), ("1024x2752", 128, 1024, 2752)]
+    per_group = []
+    if len(fs) >= 48 and len(fs) == len(ws_):
+        last_f, last_w = fs[-48:], ws_[-48:]
+        for g, (name, N, m, n) in enumerate(groups):
+            for j in range(1, 16):
+                k, fk = last_f[16 * g + j]
+                per_group.append({"group": name, "iteration": (j - 1) // 3, "kernel": k,
+                                  "read_mib_per_block": round(fk * 1024 * fscale / N / 2 ** 20, 3),
+                                  "write_mib_per_block": round(last_w[16 * g + j][1] * 1024 * wscale / N / 2 ** 20, 3)})
+    Path(out_path).write_text(json.dumps({"calibration": {"fetch_scale": fscale, "write_scale": wscale},
+                                          "kernels": kernels, "per_group": per_group}, indent=1) + "\n")
+    print(json.dumps({k: round(v["bytes"] / 1e9, 3) for k, v in kernels.items()}, indent=1))
 
 
 XCDS = 8  # MI355X: GRBM_GUI_ACTIVE is reported summed over the 8 XCDs' GRBMs
@@ -782,12 +875,18 @@ def main():
     ap.add_argument("--power", action="store_true",
                     help="only measure socket power, GFX clock and energy per step kernel")
     ap.add_argument("--power-seconds", type=float, default=2.0)
+    ap.add_argument("--traffic-summary", nargs=5,
+                    metavar=("OUT_JSON", "FETCH_CSV", "WRITE_CSV", "CAL_FETCH_CSV", "CAL_WRITE_CSV"),
+                    help="summarise rocprofv3 FETCH_SIZE / WRITE_SIZE runs into OUT_JSON (HBM bytes per dispatch)")
     ap.add_argument("--mfma-summary", nargs="+", metavar=("OUT_JSON", "CSV"),
                     help="summarise rocprofv3 counter CSVs (SQ_INSTS_MFMA, SQ_VALU_MFMA_BUSY_CYCLES, "
                          "GRBM_GUI_ACTIVE) into OUT_JSON")
     args = ap.parse_args()
     if args.mfma_summary:
         mfma_summary(args)
+        return
+    if args.traffic_summary:
+        traffic_summary(args)
         return
     if args.copy_calibration:
         x = torch.ones(2 ** 28, dtype=torch.float32, device="cuda")
