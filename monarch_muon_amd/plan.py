@@ -111,6 +111,12 @@ class GroupLaunch:
     table: torch.Tensor           # device int64 [N, 3]
     fp8_table: torch.Tensor | None
     struct: _abi.Group = field(default_factory=_abi.Group)
+    # host copy of the table and what rebuilds its grad column alone
+    rows_tab: np.ndarray | None = None    # int64 [N, 3]: param, grad, buf address of every block
+    counts: np.ndarray | None = None      # blocks per member parameter
+    kofs: np.ndarray | None = None        # block index within its parameter, per row
+    grad_block_bytes: int = 0
+    grad_dtype: torch.dtype | None = None
 
     @property
     def alpha_scale(self) -> float:
@@ -122,10 +128,17 @@ class GroupLaunch:
 
 
 class MuonPlanner:
-    """Builds and caches the per-step launch plan of the Muon group."""
+    """Builds and caches the per-step launch plan of the Muon group.
+
+    The plan depends on the parameters, momentum buffers (and FP8 metadata)
+    and on the gradients.  A training loop that drops its gradients after
+    every step (``zero_grad(set_to_none=True)``) hands over new gradient
+    tensors each step while everything else stays; then only the gradient
+    column of each group's block table is recomputed and uploaded."""
 
     def __init__(self):
         self._sig = None
+        self._gptr = None
         self._groups: list[GroupLaunch] = []
         self._ws: dict = {}
 
@@ -135,6 +148,7 @@ class MuonPlanner:
 
     def release(self) -> None:
         self._sig = None
+        self._gptr = None
         self._groups = []
         self._ws = {}
 
@@ -144,19 +158,45 @@ class MuonPlanner:
         dequantized, the parameter dtype when the buffer is created in this
         step -- used for the grouping key and, with ``ns_dtype=None``, as the
         Newton-Schulz dtype."""
-        sig = tuple((p.data_ptr(), g.data_ptr(), b.data_ptr(), p.dtype, g.dtype, b.dtype, tuple(b.shape))
-                    for p, g, b in zip(params, grads, bufs))
+        sig = tuple((p.data_ptr(), b.data_ptr(), p.dtype, b.dtype, b.shape) for p, b in zip(params, bufs))
         if fp8_meta is not None:
             sig = sig + tuple(t.data_ptr() for m in fp8_meta for t in m)
         if key_dtypes is not None:
             sig = sig + tuple(key_dtypes)
+        gptr = [(g.data_ptr(), g.dtype) for g in grads]
         if sig == self._sig:
-            return self._groups
+            if gptr == self._gptr:
+                return self._groups
+            if self._regrad(params, grads, gptr):
+                return self._groups
         keys = bufs if key_dtypes is None else [_KeyView(b, d) for b, d in zip(bufs, key_dtypes)]
         self._groups = [self._build(key, idx, params, grads, bufs, ns_dtype, fp8_meta)
                         for key, idx in plan_groups(keys).items()]
-        self._sig = sig
+        self._sig, self._gptr = sig, gptr
         return self._groups
+
+    def _regrad(self, params, grads, gptr) -> bool:
+        """New gradient tensors, everything else unchanged: recompute and upload
+        only the grad column of each table.  False (nothing changed) when a
+        gradient's dtype, shape or layout differs from what its group was
+        built for; the caller then rebuilds the plan, which validates."""
+        for gl in self._groups:
+            gd = gl.grad_dtype
+            for i in gl.members:
+                g = grads[i]
+                if g.dtype != gd or g.shape != params[i].shape or not g.is_contiguous():
+                    return False
+        for gl in self._groups:
+            gp = np.fromiter((gptr[i][0] for i in gl.members), dtype=np.int64, count=len(gl.members))
+            rows_tab = gl.rows_tab.copy()
+            rows_tab[:, 1] = np.repeat(gp, gl.counts) + gl.kofs * gl.grad_block_bytes
+            gl.rows_tab = rows_tab
+            # a new device table (the previous step's kernels may still read the old one)
+            gl.table = _h2d_int64(rows_tab, gl.key[0])
+            gl.struct.blocks = gl.table.data_ptr()
+            gl.struct.flags = _abi.GROUP_ALIGNED16 if not bool(np.any(rows_tab % 16)) else 0
+        self._gptr = gptr
+        return True
 
     def _workspace(self, rows, cols, ns_code, nblocks, device) -> Workspace:
         """One workspace per (geometry, NS dtype, device), grown to the largest
@@ -203,7 +243,8 @@ class MuonPlanner:
         if fp8_meta is not None:
             mb = np.array([tuple(t.data_ptr() for t in fp8_meta[i]) for i in idx], dtype=np.int64)
             fp8_table = _h2d_int64(np.repeat(mb, counts, axis=0) + k[:, None] * (rc // 128 * 4), device)
-        gl = GroupLaunch(key, rows, cols, nblocks, list(idx), ws, table, fp8_table)
+        gl = GroupLaunch(key, rows, cols, nblocks, list(idx), ws, table, fp8_table, rows_tab=rows_tab,
+                         counts=counts, kofs=k, grad_block_bytes=int(es[1]), grad_dtype=gd)
         s = gl.struct
         s.rows, s.cols, s.nblocks = rows, cols, nblocks
         s.param_dtype, s.grad_dtype = _abi.dtype_code(pd), _abi.dtype_code(gd)
@@ -235,24 +276,34 @@ class AdamLaunch:
     nchunks: int
     chunk: int
     fp8: torch.Tensor | None = None  # device int64 [T, 6]
+    host: np.ndarray | None = None   # host copy of `tensors`
 
 
 class AdamPlanner:
+    """Device tables of the AdamW launch; when only the gradients are new
+    tensors, only their column of the tensor table is rewritten."""
+
     def __init__(self):
         self._sig = None
+        self._gptr = None
         self._launches: list[AdamLaunch] = []
 
     def release(self) -> None:
         self._sig = None
+        self._gptr = None
         self._launches = []
 
     def plan(self, params, grads, ms, vs, fp8_meta=None) -> list[AdamLaunch]:
-        sig = tuple((p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), p.dtype, g.dtype, m.dtype, p.numel())
-                    for p, g, m, v in zip(params, grads, ms, vs))
+        sig = tuple((p.data_ptr(), m.data_ptr(), v.data_ptr(), p.dtype, m.dtype, p.numel())
+                    for p, m, v in zip(params, ms, vs))
         if fp8_meta is not None:
             sig = sig + tuple(t.data_ptr() for meta in fp8_meta for t in meta)
+        gptr = [(g.data_ptr(), g.dtype) for g in grads]
         if sig == self._sig:
-            return self._launches
+            if gptr == self._gptr:
+                return self._launches
+            if self._regrad(params, grads, gptr):
+                return self._launches
         buckets: "OrderedDict[tuple, list[int]]" = OrderedDict()
         for i, (p, g, m, v) in enumerate(zip(params, grads, ms, vs)):
             if m.dtype != v.dtype:
@@ -264,16 +315,33 @@ class AdamPlanner:
         launches = []
         chunk = 128 if fp8_meta is not None else ADAM_CHUNK
         for (device, pd, gd, sd), idx in buckets.items():
-            tens = [(params[i].data_ptr(), grads[i].data_ptr(), ms[i].data_ptr(), vs[i].data_ptr(), params[i].numel())
-                    for i in idx]
+            tens = np.array([(params[i].data_ptr(), grads[i].data_ptr(), ms[i].data_ptr(), vs[i].data_ptr(),
+                              params[i].numel()) for i in idx], dtype=np.int64).reshape(-1, 5)
             chunks = _chunk_codes([params[i].numel() for i in idx], chunk)
             f8 = [tuple(x.data_ptr() for x in fp8_meta[i]) for i in idx] if fp8_meta is not None else None
             launches.append(AdamLaunch(
                 idx, pd, gd, sd, _h2d_int64(tens, device), _h2d_int64(chunks if chunks.size else [0], device),
-                int(chunks.size), chunk, _h2d_int64(f8, device) if f8 is not None else None))
+                int(chunks.size), chunk, _h2d_int64(f8, device) if f8 is not None else None, host=tens))
         self._launches = launches
-        self._sig = sig
+        self._sig, self._gptr = sig, gptr
         return launches
+
+    def _regrad(self, params, grads, gptr) -> bool:
+        """New gradient tensors only: rewrite their column of each tensor table.
+        False when a gradient's dtype, size or layout differs from its bucket's
+        (the caller then rebuilds, which validates)."""
+        for al in self._launches:
+            for i in al.members:
+                g = grads[i]
+                if g.dtype != al.gd or g.numel() != params[i].numel() or not g.is_contiguous():
+                    return False
+        for al in self._launches:
+            host = al.host.copy()
+            host[:, 1] = np.fromiter((gptr[i][0] for i in al.members), dtype=np.int64, count=len(al.members))
+            al.host = host
+            al.tensors = _h2d_int64(host, al.tensors.device)  # the previous launch may still read the old one
+        self._gptr = gptr
+        return True
 
 
 def adamw_scalars(lr, beta1, beta2, eps, weight_decay, step) -> dict:

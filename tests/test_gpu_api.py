@@ -136,3 +136,49 @@ def test_resume_after_step_two_equals_uninterrupted(case_idx, fp8):
                 assert torch.equal(_bits(s1[k]), _bits(s2[k])), k
             else:
                 assert s1[k] == s2[k], k
+
+
+@pytest.mark.parametrize("case_idx,fp8", [(0, False), (1, True)], ids=["bf16-fp32mom", "bf16-fp8"])
+def test_fresh_gradient_tensors_each_step_equal_fixed_ones(case_idx, fp8):
+    """A training loop drops its gradients after every step
+    (``zero_grad(set_to_none=True)``, ``pretrain/src/optim/base.py:125``) and
+    the next backward allocates new ones: the planners then rewrite only the
+    gradient column of their tables.  Three steps with new gradient tensors at
+    new addresses (the old ones still alive, so no address is reused) must give
+    the bits of three steps with one fixed set of gradient tensors."""
+    case = CASES[case_idx]
+    m1, a1, b1 = make_case(case, device=DEV)
+    m2, a2, b2 = make_case(case, device=DEV)
+    o1, o2 = _opt(case, m1, a1, fp8), _opt(case, m2, a2, fp8)
+    if b1 is not None and not fp8:
+        for p, q, x, y in zip(m1, m2, b1, b2):
+            o1.state[p]["momentum_buffer"], o2.state[q]["momentum_buffer"] = x, y
+    held = []
+    for step in range(3):
+        old = [p.grad for p in m1 + a1]
+        held.append(old)
+        for p, g in zip(m1 + a1, old):
+            p.grad = g * (1.0 + 0.25 * step)        # a new tensor at a new address
+        for p, q in zip(m1 + a1, m2 + a2):
+            q.grad.copy_(p.grad)                    # the same values in the fixed tensors
+        o1.step()
+        o2.step()
+    torch.cuda.synchronize()
+    for p, q in zip(m1 + a1, m2 + a2):
+        assert torch.equal(p, q)
+        s1, s2 = o1.state[p], o2.state[q]
+        for k in s1:
+            if torch.is_tensor(s1[k]):
+                assert torch.equal(_bits(s1[k]), _bits(s2[k])), k
+    # a fourth step with a non-contiguous gradient (same values): it is read
+    # through a contiguous copy, on the gradient-only path as well
+    g = m1[0].grad
+    nc = torch.empty(g.shape[0], g.shape[2], g.shape[1], dtype=g.dtype, device=DEV).transpose(1, 2)
+    nc.copy_(g)
+    assert not nc.is_contiguous()
+    m1[0].grad = nc
+    o1.step()
+    o2.step()
+    torch.cuda.synchronize()
+    for p, q in zip(m1 + a1, m2 + a2):
+        assert torch.equal(p, q)
