@@ -493,9 +493,13 @@ def fresh_grad_leg(opt, params, steps=5):
 
 # ---------------------------------------------------------------- HBM ceiling
 def hbm_ceiling(args):
-    """Read, write and copy bandwidth of 16-B vector streams over 4 GiB
-    (mmuon_hbm_stream), swept over grid sizes and plain / non-temporal
-    accesses, beside torch's device copy.  Bytes moved = read + written."""
+    """Bandwidth of 16-B vector streams over 4 GiB buffers (mmuon_hbm_stream),
+    swept over launch sizes and plain / non-temporal accesses, beside torch's
+    device copy.  Two launch patterns: grid-stride 256-thread workgroups (4
+    accesses in flight), and 1024-thread workgroups that each stream one
+    contiguous span (8 in flight); with the spans also an in-place update
+    (read and rewrite) and the momentum pack's three streams (gradient read,
+    momentum read and rewritten, X written).  Bytes moved = read + written."""
     from monarch_muon_amd import _abi
     lib = _abi.lib()
     dev = torch.device("cuda", 0)
@@ -519,19 +523,24 @@ def hbm_ceiling(args):
             ts.append(a.elapsed_time(b))
         return statistics.median(ts)
 
+    kinds = ((0, "read", "grid-stride", 1), (1, "write", "grid-stride", 1), (2, "copy", "grid-stride", 2),
+             (3, "read", "spans", 1), (4, "write", "spans", 1), (5, "copy", "spans", 2),
+             (6, "update in place", "spans", 2), (7, "pack pattern", "spans", 3))
     rows = []
-    for kind, name, moved in ((0, "read", 1), (1, "write", 1), (2, "copy", 2)):
+    for kind, name, pattern, moved in kinds:
+        grids = (1024, 2048, 4096, 8192, 16384) if pattern == "grid-stride" else (1024, 4096, 16384, 65536)
         for nt in (0, 1):
-            for grid in (1024, 2048, 4096, 8192, 16384):
-                d = None if kind == 0 else dst.data_ptr()
+            for grid in grids:
+                d = None if kind in (0, 3) else dst.data_ptr()
                 ms = timed(lambda: _abi.check(lib.mmuon_hbm_stream(kind, d, src.data_ptr(), nbytes, nt, grid, stream),
                                               "mmuon_hbm_stream"))
-                rows.append({"kind": name, "nontemporal": nt, "grid": grid, "ms": round(ms, 4),
+                rows.append({"kind": name, "pattern": pattern, "nontemporal": nt, "grid": grid, "ms": round(ms, 4),
                              "gbs": round(moved * nbytes / (ms * 1e-3) / 1e9, 1)})
     ms = timed(lambda: dst.copy_(src))
-    rows.append({"kind": "copy", "nontemporal": None, "grid": "torch copy_", "ms": round(ms, 4),
+    rows.append({"kind": "copy", "pattern": "torch copy_", "nontemporal": None, "grid": None, "ms": round(ms, 4),
                  "gbs": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)})
-    best = {k: max((r for r in rows if r["kind"] == k), key=lambda r: r["gbs"]) for k in ("read", "write", "copy")}
+    best = {k: max((r for r in rows if r["kind"] == k), key=lambda r: r["gbs"])
+            for k in ("read", "write", "copy", "update in place", "pack pattern")}
     print(json.dumps({"metric": "HBM stream bandwidth (GB/s, read + written)", "bytes": nbytes,
                       "peak_gbs": PEAK_HBM_GBS, "best": best, "rows": rows}), flush=True)
 

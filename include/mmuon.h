@@ -298,14 +298,22 @@ int mmuon_butterfly_bwd(const mmuon_butterfly_args* a, void* stream);
 /* Workspace bytes the backward needs for these shapes (x, pointers unused). */
 size_t mmuon_butterfly_workspace(const mmuon_butterfly_args* a);
 
-/* HBM streaming probe: reads (kind 0: src), writes (kind 1: dst, hashed
-   random-looking data) or copies (kind 2: src -> dst) `bytes` with 16-B vector
-   accesses, grid x 256 threads, grid-stride; nontemporal != 0 uses
-   non-temporal loads and stores.  No counterpart in the reference: it measures
-   the bandwidth this GPU sustains, the ceiling of the step's HBM-bound kernels
-   (momentum pack, AdamW).  bytes a positive multiple of 16, buffers 16-B
-   aligned; kind 0 may pass dst = NULL (else dst holds grid * 4096 bytes). */
-int mmuon_hbm_stream(int32_t kind, void* dst, const void* src, int64_t bytes, int32_t nontemporal,
+/* HBM streaming probe with 16-B vector accesses over `bytes`-long buffers;
+   nontemporal != 0 uses non-temporal loads and stores.
+     kind 0 / 1 / 2: read src / write dst (hashed random-looking data) / copy
+       src -> dst; grid x 256 threads, grid-stride, 4 accesses in flight;
+     kind 3 / 4 / 5 / 6: read / write / copy / update dst in place; grid x 1024
+       threads, workgroup w streams the w-th of grid contiguous spans, 8
+       accesses in flight;
+     kind 7: the momentum pack's three streams over spans: per 16-B gradient
+       unit read from src's first half, two 16-B momentum units of dst read and
+       rewritten and one 16-B unit written to src's second half (3 x bytes moved).
+   No counterpart in the reference: it measures the bandwidth this GPU sustains,
+   the ceiling of the step's HBM-bound kernels (momentum pack, AdamW).  bytes a
+   positive multiple of 32, buffers 16-B aligned; the read probes may pass
+   dst = NULL (else dst holds grid * 4096 (kind 0) or grid * 16384 (kind 3)
+   bytes). */
+int mmuon_hbm_stream(int32_t kind, void* dst, void* src, int64_t bytes, int32_t nontemporal,
                      int32_t grid, void* stream);
 
 /* Thread-local message of the last failing call ("" if none). */

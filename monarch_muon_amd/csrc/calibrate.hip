@@ -80,31 +80,117 @@ void launch_probe(uint4* dst, const uint4* src, int64_t n16, bool nt, int grid, 
   else hipLaunchKernelGGL((stream_probe_kernel<KIND, false>), dim3(grid), dim3(SP_NT), 0, s, dst, src, n16);
 }
 
+// Span probes: SPAN_NT-thread workgroups, workgroup w streams the contiguous
+// chunks [w * per, (w + 1) * per), SPAN_UNROLL accesses in flight per thread.
+// KIND 3: read src; 4: write dst; 5: copy src -> dst; 6: update dst in place;
+// 7: the momentum pack's pattern: per gradient chunk i (src[i], i < n16 / 2),
+// momentum chunks 2i, 2i+1 of dst read and rewritten and X chunk n16/2 + i of
+// src written (three streams of 16-B accesses, 3 x 16 x n16 bytes in all).
+constexpr int SPAN_NT = 1024;
+constexpr int SPAN_UNROLL = 8;
+template <int KIND, bool NTA>
+__global__ __launch_bounds__(SPAN_NT) void span_probe_kernel(uint4* __restrict__ dst, uint4* __restrict__ src,
+                                                             int64_t n16, int64_t per) {
+  const uint4 key = make_uint4(0x9E3779B9u, 0x7F4A7C15u, 0xBF58476Du, 0x1CE4E5B9u);
+  if constexpr (KIND == 7) {
+    const int64_t ng = n16 / 2;
+    const int64_t b0 = int64_t(blockIdx.x) * per, b1 = min(ng, b0 + per);
+    for (int64_t i = b0 + threadIdx.x; i < b1; i += SPAN_NT) {
+      const uint4 gv = ld16(src + i, NTA);
+      uint4 m0 = ld16(dst + 2 * i, NTA), m1 = ld16(dst + 2 * i + 1, NTA);
+      m0.x ^= gv.x; m0.y += gv.y; m1.z ^= gv.z; m1.w += gv.w;
+      st16(dst + 2 * i, m0, NTA);
+      st16(dst + 2 * i + 1, m1, NTA);
+      st16(src + ng + i, make_uint4(m0.x, m0.y, m1.z, m1.w), NTA);
+    }
+    return;
+  }
+  const int64_t b0 = int64_t(blockIdx.x) * per, b1 = min(n16, b0 + per);
+  int64_t i = b0 + threadIdx.x;
+  uint4 acc = make_uint4(0, 0, 0, 0);
+  for (; i + (SPAN_UNROLL - 1) * SPAN_NT < b1; i += SPAN_UNROLL * SPAN_NT) {
+    uint4 v[SPAN_UNROLL];
+#pragma unroll
+    for (int u = 0; u < SPAN_UNROLL; ++u) {
+      if constexpr (KIND == 4) v[u] = pattern(i + u * SPAN_NT);
+      else if constexpr (KIND == 6) v[u] = ld16(dst + i + u * SPAN_NT, NTA);
+      else v[u] = ld16(src + i + u * SPAN_NT, NTA);
+    }
+#pragma unroll
+    for (int u = 0; u < SPAN_UNROLL; ++u) {
+      if constexpr (KIND == 3) {
+        acc.x ^= v[u].x; acc.y += v[u].y; acc.z ^= v[u].z; acc.w += v[u].w;
+      } else if constexpr (KIND == 6) {
+        st16(dst + i + u * SPAN_NT, make_uint4(v[u].x ^ key.x, v[u].y, v[u].z, v[u].w), NTA);
+      } else {
+        st16(dst + i + u * SPAN_NT, v[u], NTA);
+      }
+    }
+  }
+  for (; i < b1; i += SPAN_NT) {
+    if constexpr (KIND == 3) {
+      const uint4 v = ld16(src + i, NTA);
+      acc.x ^= v.x; acc.y += v.y; acc.z ^= v.z; acc.w += v.w;
+    } else if constexpr (KIND == 4) {
+      st16(dst + i, pattern(i), NTA);
+    } else if constexpr (KIND == 6) {
+      const uint4 v = ld16(dst + i, NTA);
+      st16(dst + i, make_uint4(v.x ^ key.x, v.y, v.z, v.w), NTA);
+    } else {
+      st16(dst + i, ld16(src + i, NTA), NTA);
+    }
+  }
+  if constexpr (KIND == 3) {
+    if (acc.x == key.x && acc.y == key.y && acc.z == key.z && acc.w == key.w && dst)
+      dst[int64_t(blockIdx.x) * SPAN_NT + threadIdx.x] = acc;
+  }
+}
+
+template <int KIND>
+void launch_span(uint4* dst, uint4* src, int64_t n16, bool nt, int grid, hipStream_t s) {
+  const int64_t units = KIND == 7 ? n16 / 2 : n16;
+  const int64_t per = (units + grid - 1) / grid;
+  if (nt) hipLaunchKernelGGL((span_probe_kernel<KIND, true>), dim3(grid), dim3(SPAN_NT), 0, s, dst, src, n16, per);
+  else hipLaunchKernelGGL((span_probe_kernel<KIND, false>), dim3(grid), dim3(SPAN_NT), 0, s, dst, src, n16, per);
+}
+
 }  // namespace
 }  // namespace mmuon
 
-extern "C" int mmuon_hbm_stream(int32_t kind, void* dst, const void* src, int64_t bytes, int32_t nontemporal,
+extern "C" int mmuon_hbm_stream(int32_t kind, void* dst, void* src, int64_t bytes, int32_t nontemporal,
                                 int32_t grid, void* stream) {
   using namespace mmuon;
   char msg[160];
-  if (kind < 0 || kind > 2) return set_error(MMUON_EINVAL, "kind must be 0 (read), 1 (write) or 2 (copy)");
-  if (bytes <= 0 || bytes % 16) return set_error(MMUON_EINVAL, "bytes must be a positive multiple of 16");
+  if (kind < 0 || kind > 7) return set_error(MMUON_EINVAL, "kind must be in [0, 7]");
+  if (bytes <= 0 || bytes % 32) return set_error(MMUON_EINVAL, "bytes must be a positive multiple of 32");
   if (grid < 1 || grid > (1 << 20)) return set_error(MMUON_EINVAL, "grid must be in [1, 2^20]");
-  if ((kind != 1 && src == nullptr) || (kind != 0 && dst == nullptr)) return set_error(MMUON_EINVAL, "null buffer");
+  const bool reads_src = kind == 0 || kind == 2 || kind == 3 || kind == 5 || kind == 7;
+  const bool needs_dst = kind != 0 && kind != 3;
+  if ((reads_src && src == nullptr) || (needs_dst && dst == nullptr)) return set_error(MMUON_EINVAL, "null buffer");
   if ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) % 16)
     return set_error(MMUON_EINVAL, "buffers must be 16-B aligned");
   // the read probe's improbable store lands in dst[0 .. grid * 256) when dst is given
-  if (kind == 0 && dst != nullptr && int64_t(grid) * SP_NT * 16 > bytes) {
-    snprintf(msg, sizeof msg, "read probe: dst must hold grid * 4096 bytes (%lld)", (long long)grid * SP_NT * 16);
+  const int64_t wg_threads = kind <= 2 ? SP_NT : SPAN_NT;
+  if ((kind == 0 || kind == 3) && dst != nullptr && int64_t(grid) * wg_threads * 16 > bytes) {
+    snprintf(msg, sizeof msg, "read probe: dst must hold grid * %lld bytes (%lld)", (long long)wg_threads * 16,
+             (long long)grid * wg_threads * 16);
     return set_error(MMUON_EINVAL, msg);
   }
   const int64_t n16 = bytes / 16;
   auto* d = static_cast<uint4*>(dst);
   const auto* sr = static_cast<const uint4*>(src);
+  auto* sw = static_cast<uint4*>(src);  // kind 7 writes its X stream into src's second half
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const bool nt = nontemporal != 0;
-  if (kind == 0) launch_probe<0>(d, sr, n16, nt, grid, s);
-  else if (kind == 1) launch_probe<1>(d, sr, n16, nt, grid, s);
-  else launch_probe<2>(d, sr, n16, nt, grid, s);
+  switch (kind) {
+    case 0: launch_probe<0>(d, sr, n16, nt, grid, s); break;
+    case 1: launch_probe<1>(d, sr, n16, nt, grid, s); break;
+    case 2: launch_probe<2>(d, sr, n16, nt, grid, s); break;
+    case 3: launch_span<3>(d, sw, n16, nt, grid, s); break;
+    case 4: launch_span<4>(d, sw, n16, nt, grid, s); break;
+    case 5: launch_span<5>(d, sw, n16, nt, grid, s); break;
+    case 6: launch_span<6>(d, sw, n16, nt, grid, s); break;
+    default: launch_span<7>(d, sw, n16, nt, grid, s); break;
+  }
   return launch_status("mmuon_hbm_stream");
 }

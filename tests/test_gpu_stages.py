@@ -13,7 +13,11 @@ Bar: |stage - fp64| <= 2^-8 * max|fp64| per block (one bf16 step at the largest
 entry; bf16 output rounding is at most half of that).  Diagonal 256 x 256 tiles
 of A and P are stored in full and must be exactly symmetric.  The shapes cover
 m = 1024 (four diagonal tiles per block, whose 32 x 32 MFMA tiles the kernels
-deal over the waves), tall and wide blocks, and zero padding.
+deal over the waves), tall and wide blocks, and zero padding; the two largest
+stacks have more tiles than the 256 persistent workgroups, so a workgroup runs
+several tiles in a row (diagonal and upper tiles, tiles of different blocks)
+through the same LDS ring and staging area.  The fp64 reference products run
+on the GPU.
 """
 import ctypes as C
 
@@ -26,13 +30,14 @@ from monarch_muon_amd.plan import NS_COEFFS, MuonPlanner
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
 TILE = 256
-SHAPES = [(2, 1024, 1024), (1, 2752, 1024), (1, 1024, 2752), (3, 512, 512), (2, 96, 136)]
+SHAPES = [(2, 1024, 1024), (1, 2752, 1024), (1, 1024, 2752), (3, 512, 512), (2, 96, 136),
+          (40, 1024, 1024), (30, 1024, 2752)]
 
 
 def panels(t: torch.Tensor, nblocks: int, rows: int, cols: int) -> torch.Tensor:
     """A bf16 stack in 32-column panels ([N][cols/32][rows][32]) as row-major fp64 [N, rows, cols]."""
     v = t.view(torch.bfloat16)[: nblocks * rows * cols].view(nblocks, cols // 32, rows, 32)
-    return v.permute(0, 2, 1, 3).reshape(nblocks, rows, cols).double().cpu()
+    return v.permute(0, 2, 1, 3).reshape(nblocks, rows, cols).double()
 
 
 def mirror_upper(a: torch.Tensor) -> torch.Tensor:
@@ -79,7 +84,7 @@ def test_stage_outputs_against_fp64_products(shape):
 
     _abi.check(lib.mmuon_momentum_pack(C.byref(gl.struct), 0.0, stream), "pack")  # X = bf16(g), s = 1/||X||
     torch.cuda.synchronize()
-    s = ws.scale.double().cpu().view(nb, 1, 1)
+    s = ws.scale.double().view(nb, 1, 1)
     x = panels(ws.x0, nb, mp, np_)
 
     stage(0, 0)  # SYRK of the first iteration (scaled by s^2)
@@ -89,7 +94,7 @@ def test_stage_outputs_against_fp64_products(shape):
     stage(0, 1)  # POLY from the stored A
     full_a = mirror_upper(a)
     pm = panels(ws.p, nb, mp, mp)
-    eye = torch.zeros(mp, mp, dtype=torch.float64)
+    eye = torch.zeros(mp, mp, dtype=torch.float64, device=DEV)
     eye[range(lay.m), range(lay.m)] = 1.0
     check_upper_tiles(pm, a_c * eye + b_c * full_a + c_c * (full_a @ full_a), "POLY")
     # the padding rows and columns of P stay zero, its diagonal included
