@@ -307,7 +307,8 @@ size_t mmuon_butterfly_workspace(const mmuon_butterfly_args* a);
        accesses in flight;
      kind 7: the momentum pack's three streams over spans: per 16-B gradient
        unit read from src's first half, two 16-B momentum units of dst read and
-       rewritten and one 16-B unit written to src's second half (3 x bytes moved).
+       rewritten and one 16-B unit written to src's second half (3 x bytes
+       moved), two gradient units in flight per thread.
    No counterpart in the reference: it measures the bandwidth this GPU sustains,
    the ceiling of the step's HBM-bound kernels (momentum pack, AdamW).  bytes a
    positive multiple of 32, buffers 16-B aligned; the read probes may pass

@@ -17,8 +17,13 @@ __device__ __forceinline__ uint4 ld16(const uint4* p, bool nt) {
   return nt ? load16_nt(p) : *p;
 }
 __device__ __forceinline__ void st16(uint4* p, const uint4& v, bool nt) {
-  if (nt) store16_nt(p, v);
-  else *p = v;
+  if (nt) {
+    store16_nt(p, v);
+  } else {
+    // one 16-B store (an ext-vector store keeps the four words together)
+    const u32x4_nt r = {v.x, v.y, v.z, v.w};
+    *reinterpret_cast<u32x4_nt*>(p) = r;
+  }
 }
 
 // Data written by the write probe: a 64-bit multiplicative hash of the chunk
@@ -93,16 +98,33 @@ __global__ __launch_bounds__(SPAN_NT) void span_probe_kernel(uint4* __restrict__
                                                              int64_t n16, int64_t per) {
   const uint4 key = make_uint4(0x9E3779B9u, 0x7F4A7C15u, 0xBF58476Du, 0x1CE4E5B9u);
   if constexpr (KIND == 7) {
+    // PACK_UNROLL gradient units (three loads each) in flight per thread
+    constexpr int PACK_UNROLL = 2;
     const int64_t ng = n16 / 2;
     const int64_t b0 = int64_t(blockIdx.x) * per, b1 = min(ng, b0 + per);
-    for (int64_t i = b0 + threadIdx.x; i < b1; i += SPAN_NT) {
-      const uint4 gv = ld16(src + i, NTA);
-      uint4 m0 = ld16(dst + 2 * i, NTA), m1 = ld16(dst + 2 * i + 1, NTA);
-      m0.x ^= gv.x; m0.y += gv.y; m1.z ^= gv.z; m1.w += gv.w;
-      st16(dst + 2 * i, m0, NTA);
-      st16(dst + 2 * i + 1, m1, NTA);
-      st16(src + ng + i, make_uint4(m0.x, m0.y, m1.z, m1.w), NTA);
+    int64_t i = b0 + threadIdx.x;
+    // every word of the three written units changes (a unit stored back
+    // unchanged could be dropped by the compiler)
+    auto one = [&](int64_t k, const uint4& gv, uint4 m0, uint4 m1) {
+      m0.x ^= gv.x; m0.y += gv.y; m0.z ^= gv.z; m0.w += gv.w;
+      m1.x += gv.x; m1.y ^= gv.y; m1.z += gv.z; m1.w ^= gv.w;
+      st16(dst + 2 * k, m0, NTA);
+      st16(dst + 2 * k + 1, m1, NTA);
+      st16(src + ng + k, make_uint4(m0.x ^ m1.x, m0.y ^ m1.y, m0.z ^ m1.z, m0.w ^ m1.w), NTA);
+    };
+    for (; i + (PACK_UNROLL - 1) * SPAN_NT < b1; i += PACK_UNROLL * SPAN_NT) {
+      uint4 gv[PACK_UNROLL], m0[PACK_UNROLL], m1[PACK_UNROLL];
+#pragma unroll
+      for (int u = 0; u < PACK_UNROLL; ++u) {
+        const int64_t k = i + u * SPAN_NT;
+        gv[u] = ld16(src + k, NTA);
+        m0[u] = ld16(dst + 2 * k, NTA);
+        m1[u] = ld16(dst + 2 * k + 1, NTA);
+      }
+#pragma unroll
+      for (int u = 0; u < PACK_UNROLL; ++u) one(i + u * SPAN_NT, gv[u], m0[u], m1[u]);
     }
+    for (; i < b1; i += SPAN_NT) one(i, ld16(src + i, NTA), ld16(dst + 2 * i, NTA), ld16(dst + 2 * i + 1, NTA));
     return;
   }
   const int64_t b0 = int64_t(blockIdx.x) * per, b1 = min(n16, b0 + per);
@@ -121,7 +143,7 @@ __global__ __launch_bounds__(SPAN_NT) void span_probe_kernel(uint4* __restrict__
       if constexpr (KIND == 3) {
         acc.x ^= v[u].x; acc.y += v[u].y; acc.z ^= v[u].z; acc.w += v[u].w;
       } else if constexpr (KIND == 6) {
-        st16(dst + i + u * SPAN_NT, make_uint4(v[u].x ^ key.x, v[u].y, v[u].z, v[u].w), NTA);
+        st16(dst + i + u * SPAN_NT, make_uint4(v[u].x ^ key.x, v[u].y ^ key.y, v[u].z ^ key.z, v[u].w ^ key.w), NTA);
       } else {
         st16(dst + i + u * SPAN_NT, v[u], NTA);
       }
@@ -135,7 +157,7 @@ __global__ __launch_bounds__(SPAN_NT) void span_probe_kernel(uint4* __restrict__
       st16(dst + i, pattern(i), NTA);
     } else if constexpr (KIND == 6) {
       const uint4 v = ld16(dst + i, NTA);
-      st16(dst + i, make_uint4(v.x ^ key.x, v.y, v.z, v.w), NTA);
+      st16(dst + i, make_uint4(v.x ^ key.x, v.y ^ key.y, v.z ^ key.z, v.w ^ key.w), NTA);
     } else {
       st16(dst + i, ld16(src + i, NTA), NTA);
     }
