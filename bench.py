@@ -28,6 +28,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes as C
+import gc
 import json
 import os
 import statistics
@@ -203,6 +204,17 @@ def hbm_traffic(workload, kernel):
 CPU_SAMPLE_LAYERS = 4
 
 
+def freeze_gc():
+    """Collect, then move every object alive now (torch's ~170K import-time
+    objects, the workload) into the collector's permanent generation, so a full
+    collection -- 50-70 ms of host time -- cannot land inside a timed region
+    while the GPU queue is still short (it showed as one ~125 ms step right after
+    the warm-up).  The collector stays enabled for new objects.  Called before
+    the warm-up, so the timed steps follow the warm-up without an idle gap."""
+    gc.collect()
+    gc.freeze()
+
+
 def host_cpu_info(threads):
     """What the CPU baseline ran on: model string, logical CPUs this process
     may use, the physical cores behind them, and the threads used."""
@@ -365,6 +377,7 @@ def bench_butterfly(args, w):
         for name, x, w1, w2, d in reversed(layer):
             butterfly_blk_bwd_op(x, w1, w2, saved[name], d)
 
+    freeze_gc()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -925,6 +938,7 @@ def main():
     dev = torch.device("cuda", 0)
     log(f"[bench] building workload {w.name} on {torch.cuda.get_device_name(dev)}")
     muon, adamw, opt = build_gpu(w, dev)
+    freeze_gc()
     log(f"[bench] warm-up {args.warmup} steps")
     for _ in range(args.warmup):
         if args.grad_clip:
@@ -945,7 +959,8 @@ def main():
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     step_ms = [s.elapsed_time(e) for s, e in evs]
     median_ms = statistics.median(step_ms)
-    log(f"[bench] {wall_ms:.2f} ms/step (wall), median event {median_ms:.2f} ms")
+    log(f"[bench] {wall_ms:.2f} ms/step (wall), median event {median_ms:.2f} ms; per-step events (ms): "
+        + " ".join(f"{v:.1f}" for v in step_ms))
 
     # per-kernel timing
     per = defaultdict(lambda: [0.0, 0, 0.0, 0.0])   # symbol -> [ms, launches, alg flops, exec flops]
@@ -990,7 +1005,10 @@ def main():
                    "newton_schulz": "bf16 MFMA, fp32 accumulate, 5 iterations",
                    "groups": [f"{gl.rows}x{gl.cols}x{gl.nblocks}" for gl in opt._muon_planner.groups]},
         "median_event_ms": round(median_ms, 3),
-        "statistics": {"value": "wall-clock mean of the K timed steps between two device synchronisations",
+        "event_ms": {"min": round(min(step_ms), 3), "mean": round(statistics.mean(step_ms), 3),
+                     "median": round(median_ms, 3), "max": round(max(step_ms), 3)},
+        "statistics": {"value": "wall-clock mean of the K timed steps between two device synchronisations "
+                                "(the Python collector's existing objects frozen before timing)",
                        "median_event_ms": "median of per-step hipEvent pairs, the reference harness's statistic "
                                           "(benchmark_train_step.py:297-299,386-397: 3 warm-ups, median of 12 "
                                           "event-timed steps; this script's defaults)"},
