@@ -12,6 +12,7 @@ namespace mmuon {
 
 constexpr float FP8_MAX = 448.0f;
 constexpr float QEPS = 1e-30f;
+constexpr float LOG2_QEPS = -99.657842847f;  // log2(QEPS)
 constexpr float EXPAND_MIN = 16.0f;
 
 // e4m3fn byte -> fp32 (exact).
@@ -136,9 +137,9 @@ __device__ __forceinline__ void fp8_dequant_lane(const uint4 (&codes)[E / 16], c
 
 // coat_state_muon.py:46-91 for one group (nvalid: this lane's elements that
 // exist).  Returns the group metadata (valid in every lane of the group) and
-// this lane's E codes.  The normalised value is multiplied by 1/scale rather
-// than divided by scale, and scale's power uses pow_pos (both visible only at
-// e4m3 rounding ties).
+// this lane's E codes.  Each element's power and its division by scale are one
+// exp2 of a log-domain expression, and scale's power uses pow_pos (both visible
+// only at e4m3 rounding ties).
 template <int E>
 __device__ __forceinline__ Fp8Meta fp8_quant_group(const float (&x)[E], int nvalid, bool sgn, uint4 (&codes)[E / 16]) {
   float amax = 0.f, amin = 3.4028235e38f;
@@ -162,15 +163,18 @@ __device__ __forceinline__ Fp8Meta fp8_quant_group(const float (&x)[E], int nval
   const float expand = ratio <= 1.0f + QEPS ? 1.0f : fmaxf(raw_expand, 1.0f / EXPAND_MIN);
   const float smm = fmaxf(sqrtf(amax) * sqrtf(amin), QEPS);
   const float scale = fmaxf(pow_pos(fmaxf(amax / smm, QEPS), expand) / FP8_MAX, QEPS);
-  const float inv_smm = 1.0f / smm, inv_scale = 1.0f / scale;
+  // per element, in the log domain: (max(a / smm, QEPS))^expand / scale =
+  // 2^(expand * max(log2 a - log2 smm, log2 QEPS) - log2 scale)
+  const float lsmm = __builtin_amdgcn_logf(smm), lsc = __builtin_amdgcn_logf(scale);
   float y[E];
 #pragma unroll
   for (int k = 0; k < E; ++k) {
     const float a = fabsf(x[k]);
-    const float np = pow_pos(fmaxf(a * inv_smm, QEPS), expand);
+    const float t = fmaxf(__builtin_amdgcn_logf(a) - lsmm, LOG2_QEPS);
+    const float np = __builtin_amdgcn_exp2f(fmaf(expand, t, -lsc));
     float nrm = 0.f;
     if (k < nvalid && a > 0.f) nrm = sgn ? copysignf(np, x[k]) : np;
-    y[k] = __builtin_amdgcn_fmed3f(nrm * inv_scale, -FP8_MAX, FP8_MAX);
+    y[k] = __builtin_amdgcn_fmed3f(nrm, -FP8_MAX, FP8_MAX);
   }
 #pragma unroll
   for (int h = 0; h < E / 16; ++h)
