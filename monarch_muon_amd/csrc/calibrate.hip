@@ -1,7 +1,7 @@
-// HBM streaming probes: the read, write and copy bandwidth this GPU sustains
-// for 16-B vector accesses, the ceiling the momentum pack and AdamW (both
-// HBM-bound streaming kernels) are measured against.  Not part of the
-// optimizer step.
+// HBM streaming probes: the read, write, copy, in-place update and
+// momentum-pack-pattern bandwidth this GPU sustains for 16-B vector accesses,
+// the ceilings the momentum pack and AdamW (both HBM-bound streaming kernels)
+// are measured against.  Not part of the optimizer step.
 #include <stdio.h>
 
 #include "common.hpp"
