@@ -247,18 +247,19 @@ def cpu_baseline(w, seed=0):
     of the first CPU_SAMPLE_LAYERS transformer layers plus the same fraction of
     the AdamW elements; scaled to one full step."""
     from oracle.step import ReferenceMonarchMuon
-    from monarch_muon_amd.workloads import parameter_inventory
+    from monarch_muon_amd.workloads import local_layers, parameter_inventory
     allowed = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     threads = max(1, min(16, allowed))
     torch.set_num_threads(threads)
-    layers = min(CPU_SAMPLE_LAYERS, w.n_layer)
+    nl = local_layers(w)
+    layers = min(CPU_SAMPLE_LAYERS, nl)
     gen = torch.Generator().manual_seed(seed)
     muon, adamw, bufs = [], [], []
     for name, shape, is_muon in parameter_inventory(w):
         if ".h." in name and int(name.split(".")[2]) >= layers:
             continue
-        if not is_muon and len(shape) == 2:
-            shape = (max(1, shape[0] * layers // w.n_layer), shape[1])
+        if not is_muon and (len(shape) == 2 or w.shards > 1):
+            shape = (max(1, shape[0] * layers // nl), *shape[1:])
         p = (torch.randn(shape, generator=gen) * 0.02).to(w.param_dtype).requires_grad_(True)
         p.grad = (torch.randn(shape, generator=gen) * 1e-3).to(w.param_dtype)
         (muon if is_muon else adamw).append(p)
@@ -275,9 +276,9 @@ def cpu_baseline(w, seed=0):
         opt.step()
         times.append(time.perf_counter() - t0)
     sample_ms = statistics.median(times) * 1e3
-    scale = w.n_layer / layers
+    scale = nl / layers
     return {"value": round(sample_ms * scale, 1), "unit": "ms", "cores": threads, "kind": "port",
-            "sample": f"oracle step (torch CPU) over the Muon blocks of layers 0-{layers - 1} + {layers}/{w.n_layer} "
+            "sample": f"oracle step (torch CPU) over the Muon blocks of layers 0-{layers - 1} + {layers}/{nl} "
                       f"of the AdamW elements, median of 3 after 1 warm-up = {sample_ms:.1f} ms, x{scale:g}",
             **host_cpu_info(threads)}
 
@@ -922,7 +923,7 @@ def main():
               "this build (a sharded step would give each GPU its own share of the Newton-Schulz blocks).",
               file=sys.stderr)
         sys.exit(2)
-    from monarch_muon_amd.workloads import WORKLOADS, adamw_elements, muon_elements, ns_flops
+    from monarch_muon_amd.workloads import WORKLOADS, adamw_elements, local_layers, muon_elements, ns_flops
     if args.hbm_ceiling:
         hbm_ceiling(args)
         return
@@ -998,6 +999,8 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,.02) weights, N(0,1e-3) grads and momentum, resident in HBM)",
         "config": {"workload": w.name, "layers": w.n_layer, "hidden": w.n_embd, "intermediate": w.intermediate,
+                   **({"shard": f"rank 0 of {w.shards}: the Muon blocks of layers 0-{local_layers(w) - 1} and 1/{w.shards} "
+                                f"of the AdamW group's elements"} if w.shards > 1 else {}),
                    "nblocks": w.nblocks, "muon_elements": muon_elements(w), "adamw_elements": adamw_elements(w),
                    "param_dtype": str(w.param_dtype).split(".")[-1],
                    "momentum_dtype": w.momentum_dtype if isinstance(w.momentum_dtype, str)

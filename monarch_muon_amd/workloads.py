@@ -8,7 +8,7 @@ Muon/AdamW split of ``pretrain/src/main.py:156-165``.
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass
+from dataclasses import dataclass, replace
 
 import torch
 
@@ -27,6 +27,7 @@ class Workload:
     momentum_dtype: torch.dtype | str     # torch dtype, or "fp8" for e4m3 states
     ns_dtype: torch.dtype | None          # None: Newton-Schulz in the momentum dtype
     prefill_momentum: bool                # momentum N(0, 1e-3) before step 1 (else zeros)
+    shards: int = 1                       # > 1: one rank's share of a block-ownership sharded step
 
 
 WORKLOADS = {
@@ -42,6 +43,11 @@ WORKLOADS = {
     # momentum (membench/scripts/monarch_benchmark/benchmark_train_step.py:428-436 asserts bf16 states)
     "6.89b-nb4-bf16mom": Workload("6.89b-nb4-bf16mom", 32, 4096, 32, 11008, 4, torch.bfloat16, torch.bfloat16,
                                   torch.bfloat16, True),
+    # one rank's share of the headline step sharded over 8 GPUs by block ownership: the Muon blocks of 4 of the
+    # 32 layers (every layer has the same blocks, so whole layers balance the Newton-Schulz work) and 1/8 of the
+    # AdamW group's elements (AdamW is elementwise; a rank owns a contiguous range of the flattened group)
+    "6.89b-nb4-shard8": Workload("6.89b-nb4-shard8", 32, 4096, 32, 11008, 4, torch.bfloat16, torch.float32,
+                                 torch.bfloat16, True, shards=8),
 }
 
 
@@ -60,8 +66,25 @@ def factor_shapes(d_in: int, d_out: int, nb: int):
     return (nb, ob, ib), (nb, ob, ob)
 
 
+def local_layers(w: Workload) -> int:
+    """Transformer layers whose Muon blocks the workload holds (a rank's share when sharded)."""
+    if w.n_layer % w.shards:
+        raise ValueError(f"{w.name}: {w.n_layer} layers do not split over {w.shards} ranks")
+    return w.n_layer // w.shards
+
+
 def parameter_inventory(w: Workload):
-    """Ordered ``[(name, shape, is_muon)]`` of the Monarch LLaMA's parameters."""
+    """Ordered ``[(name, shape, is_muon)]`` of the Monarch LLaMA's parameters.
+
+    A sharded workload (``shards`` > 1) is rank 0's share: the Muon blocks of
+    layers ``[0, n_layer / shards)`` and one flat tensor holding its
+    ``ceil(1 / shards)`` range of the AdamW group's elements."""
+    if w.shards > 1:
+        full = replace(w, shards=1)
+        share = -(-adamw_elements(full) // w.shards)
+        muon = [(n, s, m) for n, s, m in parameter_inventory(full)
+                if m and int(n.split(".")[2]) < local_layers(w)]
+        return muon + [("adamw_group.elements_of_rank_0", (share,), False)]
     h, hid, nb = w.n_embd, mlp_hidden(w.n_embd, w.intermediate), w.nblocks
     out = [("transformer.wte.weight", (VOCAB, h))]
     for li in range(w.n_layer):

@@ -61,3 +61,19 @@ def test_adamw_scalars_are_python_doubles():
     assert s["sqrt_bc2"] == math.sqrt(1 - 0.95 ** 3)
     assert s["wd_factor"] == 1 - 1e-3 * 0.1 and s["apply_weight_decay"] == 1
     assert adamw_scalars(1e-3, 0.9, 0.95, 1e-8, 0.0, 1)["apply_weight_decay"] == 0
+
+
+def test_shard_workload_is_one_eighth_of_the_headline_step():
+    """Rank 0's share of an 8-way block-ownership step: the Muon blocks of 4 of
+    the 32 layers (one eighth of every shape group, in the same order) and one
+    eighth of the AdamW elements; one eighth of the Newton-Schulz work."""
+    full, shard = WORKLOADS["6.89b-nb4"], WORKLOADS["6.89b-nb4-shard8"]
+    inv = parameter_inventory(shard)
+    mu = [s for _, s, m in inv if m]
+    bufs = [torch.empty(s, device="meta") for s in mu]
+    planned = [(k[2], k[3], sum(bufs[i].shape[0] for i in idx)) for k, idx in plan_groups(bufs).items()]
+    assert planned == [(r, c, n // 8) for r, c, n in APPENDIX_B["6.89b-nb4"][2]]
+    assert [n for n, _, m in inv if m] == [n for n, _, m in parameter_inventory(full) if m][: len(mu)]
+    assert muon_elements(shard) * 8 == muon_elements(full)
+    assert adamw_elements(shard) == -(-adamw_elements(full) // 8)
+    assert abs(ns_flops(shard) * 8 - ns_flops(full)) < 1e3
