@@ -219,13 +219,14 @@ def host_cpu_info(threads):
     """What the CPU baseline ran on: model string, logical CPUs this process
     may use, the physical cores behind them, and the threads used."""
     model, cores = "", set()
-    cur = {}
+    cur, first = {}, {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if not line.strip():
                     if "processor" in cur:
                         cores.add((int(cur["processor"]), cur.get("physical id", "0"), cur.get("core id", cur["processor"])))
+                        first = first or cur
                     cur = {}
                     continue
                 k, _, v = line.partition(":")
@@ -238,7 +239,12 @@ def host_cpu_info(threads):
         pass
     allowed = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
     phys = {(pid, cid) for proc, pid, cid in cores if proc in allowed}
-    return {"cpu_model": model, "threads": threads, "logical_cpus_allowed": len(allowed),
+    flags = set(first.get("flags", "").split())
+    names = {"vendor_id": "cpu_vendor", "cpu family": "cpu_family", "model": "cpu_model_number",
+             "stepping": "cpu_stepping", "cpu MHz": "cpu_mhz"}
+    ident = {v: first[k] for k, v in names.items() if k in first}
+    return {"cpu_model": model, **ident, "hypervisor": "hypervisor" in flags,
+            "avx512_bf16": "avx512_bf16" in flags, "threads": threads, "logical_cpus_allowed": len(allowed),
             "physical_cores_allowed": len(phys) or None, "os_cpu_count": os.cpu_count()}
 
 
