@@ -164,7 +164,7 @@ def stage_exec_flops(kind, gl):
     N, mp, np_ = gl.nblocks, lay.mp, lay.np_
     nt = mp // 256
     sym = (nt * (nt - 1) / 2 + nt * 36 / 64) / (nt * nt)
-    kx = -(-lay.n // 64) * 64
+    kx = -(-lay.n // 32) * 32   # SYRK's K: n rounded up to the 32-deep slices
     if kind == "syrk":
         return 2.0 * mp * mp * kx * N * sym
     if kind == "poly":
@@ -647,6 +647,70 @@ class PowerSampler:
         return {"socket_w": mean(1), "gfx_mhz": mean(2), "avg_gfx_mhz": mean(3), "samples": len(s)}
 
 
+def stage_bytes(kind, gl):
+    """Algorithmic HBM bytes of one launch of a Newton-Schulz stage over the
+    stored extents: bf16 X stacks (m_p x K rows x columns read, m_p x n_p
+    written), the upper 256 x 256 tiles of A and P, and for the last PX the
+    parameter block read and written instead of X'."""
+    lay = gl.ws.layout
+    N, mp, np_ = gl.nblocks, lay.mp, lay.np_
+    nt = mp // 256
+    up = nt * (nt + 1) // 2 * 256 * 256 * 2
+    kx = -(-lay.n // 32) * 32
+    xin = mp * kx * 2
+    if kind == "syrk":
+        return N * (xin + up)
+    if kind == "poly":
+        return N * 2 * up
+    if kind == "px":
+        return N * (up + xin + mp * np_ * 2)
+    pb = 2 if gl.struct.param_dtype == 1 else 4
+    return N * (up + xin + 2 * gl.rows * gl.cols * pb)
+
+
+def stage_table(args, w):
+    """Per group: each Newton-Schulz stage launched back to back (the second
+    iteration's SYRK, POLY and PX, the last iteration's PX with the update),
+    median over 3 loops of 20 launches, with its algorithmic HBM bytes and
+    executed MFMA FLOPs per launch."""
+    from monarch_muon_amd import _abi
+    from monarch_muon_amd.optim import _COEFFS
+    from monarch_muon_amd.plan import NS_STEPS
+    dev = torch.device("cuda", 0)
+    muon, adamw, opt = build_gpu(w, dev)
+    opt.step()
+    torch.cuda.synchronize()
+    lib = _abi.lib()
+    stream = _abi.stream_handle(dev)
+    rows = []
+    for gl in opt._muon_planner.groups:
+        for kind, it, st in (("syrk", 1, 0), ("poly", 1, 1), ("px", 1, 2), ("px_apply", NS_STEPS - 1, 2)):
+            def launch():
+                _abi.check(lib.mmuon_ns_stage(C.byref(gl.struct), it, NS_STEPS, st, _COEFFS,
+                                              -0.02 * gl.alpha_scale, 0, stream), "mmuon_ns_stage")
+            launch()
+            torch.cuda.synchronize()
+            loops = []
+            for _ in range(3):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(20):
+                    launch()
+                e1.record()
+                torch.cuda.synchronize()
+                loops.append(e0.elapsed_time(e1) / 20)
+            ms = statistics.median(loops)
+            nbytes = stage_bytes(kind, gl)
+            ex = stage_exec_flops("px" if kind == "px_apply" else kind, gl)
+            rows.append({"group": f"{gl.rows}x{gl.cols}x{gl.nblocks}", "stage": kind, "ms": round(ms, 4),
+                         "alg_bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
+                         "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
+                         "exec_tflops": round(ex / ms / 1e9, 1),
+                         "frac_mfma": round(ex / ms / 1e9 / PEAK_BF16_TFLOPS, 4)})
+            log(f"[stages] {rows[-1]}")
+    print(json.dumps({"workload": w.name, "stages": rows}))
+
+
 def power_profile(args, w):
     """Each kernel of one optimizer step on the 1024 x 1024 group (and the
     AdamW group, and the whole step) launched back to back for about two
@@ -904,6 +968,8 @@ def main():
     ap.add_argument("--power", action="store_true",
                     help="only measure socket power, GFX clock and energy per step kernel")
     ap.add_argument("--power-seconds", type=float, default=2.0)
+    ap.add_argument("--stage-table", action="store_true",
+                    help="time each Newton-Schulz stage per group: ms, algorithmic GB/s, executed TFLOP/s")
     ap.add_argument("--traffic-summary", nargs=5,
                     metavar=("OUT_JSON", "FETCH_CSV", "WRITE_CSV", "CAL_FETCH_CSV", "CAL_WRITE_CSV"),
                     help="summarise rocprofv3 FETCH_SIZE / WRITE_SIZE runs into OUT_JSON (HBM bytes per dispatch)")
@@ -935,6 +1001,9 @@ def main():
         return
     if args.power:
         power_profile(args, WORKLOADS[args.workload])
+        return
+    if args.stage_table:
+        stage_table(args, WORKLOADS[args.workload])
         return
     if args.workload.startswith("butterfly-"):
         model = args.workload[len("butterfly-"):]
