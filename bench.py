@@ -106,14 +106,14 @@ def instrumented_step(opt, lr=0.02):
             _abi.check(lib.mmuon_momentum_pack(C.byref(gl.struct), 0.95, stream), "pack")
         e1.record()
         out.append(("pack", gl, 0, e0, e1))
-        for it in range(NS_STEPS):
-            for st in range(3):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record()
-                _abi.check(lib.mmuon_ns_stage(C.byref(gl.struct), it, NS_STEPS, st, _COEFFS,
-                                              -lr * gl.alpha_scale, 0, stream), "ns_stage")
-                e1.record()
-                out.append((("syrk", "poly", "px")[st], gl, it, e0, e1))
+        # the launches of mmuon_newton_schulz_apply, one op at a time
+        for op in _abi.ns_plan(gl.rows, gl.cols, gl.struct.ns_dtype, NS_STEPS, opt._ns_flags):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            _abi.check(lib.mmuon_ns_run_op(C.byref(gl.struct), C.byref(op), _COEFFS, -lr * gl.alpha_scale,
+                                           stream), "mmuon_ns_run_op")
+            e1.record()
+            out.append((OP_KIND[op.kind], gl, op.iteration, e0, e1))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     opt._adamw_step(adam_group, lr)
@@ -123,20 +123,27 @@ def instrumented_step(opt, lr=0.02):
     return [(k, gl, it, e0.elapsed_time(e1)) for k, gl, it, e0, e1 in out]
 
 
+# Newton-Schulz plan op kinds (MMUON_NSOP_*) by name
+OP_KIND = {0: "syrk", 1: "poly", 2: "px", 3: "px_apply", 4: "symm"}
+NS_KINDS = ("syrk", "poly", "symm", "px", "px_apply")
+
+
 def kernel_symbol(kind, gl, it, fp8=False):
     """The kernel (template instance) rocprof reports for a launch, as it
     appears in ``rocprofv3 --stats`` names (mmuon::(anonymous namespace)::...)."""
     tp = "BF16T" if gl is not None and gl.struct.param_dtype == 1 else "F32T"
-    if gl is not None and kind in ("syrk", "poly", "px") and gl.struct.ns_dtype == 0:  # fp32 Newton-Schulz
-        stage = {"syrk": 0, "poly": 1}.get(kind, 2 if it < 4 else 3)
+    if gl is not None and kind in NS_KINDS and gl.struct.ns_dtype == 0:  # fp32 Newton-Schulz
+        stage = {"syrk": 0, "poly": 1, "px": 2, "px_apply": 3}[kind]
         return f"ns_f32<{stage}, {tp if stage == 3 else 'F32T'}>"
     if kind == "syrk":
         return "ns_sym_bf16<0>"
     if kind == "poly":
         return "ns_sym_bf16<1>"
+    if kind == "symm":
+        return "ns_sym_bf16<4>"
     if kind == "px":
-        if it < 4:
-            return "ns_px_bf16<2, false, BF16T>"
+        return "ns_px_bf16<2, false, BF16T>"
+    if kind == "px_apply":
         return f"ns_px_bf16<3, {'true' if gl.transposed else 'false'}, {tp}>"
     if kind == "pack":
         return ("fp8_" if fp8 else "") + ("pack_cols_kernel" if gl.transposed else "pack_rows_kernel")
@@ -144,14 +151,14 @@ def kernel_symbol(kind, gl, it, fp8=False):
 
 
 def stage_flops(kind, gl):
-    """Algorithmic FLOPs of one launch (full products, symmetry not credited)."""
+    """Algorithmic FLOPs of one launch (its full product, symmetry not credited)."""
     lay = gl.ws.layout
     m, n, N = lay.m, lay.n, gl.nblocks
     if kind == "syrk":
         return 2.0 * m * m * n * N
-    if kind == "poly":
+    if kind in ("poly", "symm"):
         return 2.0 * m * m * m * N
-    if kind == "px":
+    if kind in ("px", "px_apply"):
         return 2.0 * m * m * n * N
     return 0.0
 
@@ -167,11 +174,17 @@ def stage_exec_flops(kind, gl):
     kx = -(-lay.n // 32) * 32   # SYRK's K: n rounded up to the 32-deep slices
     if kind == "syrk":
         return 2.0 * mp * mp * kx * N * sym
-    if kind == "poly":
+    if kind in ("poly", "symm"):
         return 2.0 * mp * mp * mp * N * sym
-    if kind == "px":
+    if kind in ("px", "px_apply"):
         return 2.0 * mp * mp * np_ * N
     return 0.0
+
+
+def _ns_plan(gl, opt):
+    from monarch_muon_amd import _abi
+    from monarch_muon_amd.plan import NS_STEPS
+    return _abi.ns_plan(gl.rows, gl.cols, gl.struct.ns_dtype, NS_STEPS, opt._ns_flags)
 
 
 def pack_bytes(gl, momentum_bytes, grad_bytes=2, x_bytes=2):
@@ -662,6 +675,8 @@ def stage_bytes(kind, gl):
         return N * (xin + up)
     if kind == "poly":
         return N * 2 * up
+    if kind == "symm":
+        return N * 3 * up
     if kind == "px":
         return N * (up + xin + mp * np_ * 2)
     pb = 2 if gl.struct.param_dtype == 1 else 4
@@ -683,9 +698,17 @@ def stage_table(args, w):
     lib = _abi.lib()
     stream = _abi.stream_handle(dev)
     rows = []
+    symm = _abi.NsOp(_abi.NSOP_SYMM, _abi.NSB_P, _abi.NSB_A, _abi.NSB_X1_S0, 0, 0)
     for gl in opt._muon_planner.groups:
-        for kind, it, st in (("syrk", 1, 0), ("poly", 1, 1), ("px", 1, 2), ("px_apply", NS_STEPS - 1, 2)):
+        stages = [("syrk", 1, 0), ("poly", 1, 1), ("px", 1, 2), ("px_apply", NS_STEPS - 1, 2)]
+        if any(op.kind == _abi.NSOP_SYMM for op in _ns_plan(gl, opt)):
+            stages.insert(2, ("symm", 1, -1))
+        for kind, it, st in stages:
             def launch():
+                if st < 0:
+                    _abi.check(lib.mmuon_ns_run_op(C.byref(gl.struct), C.byref(symm), _COEFFS, 0.0, stream),
+                               "mmuon_ns_run_op")
+                    return
                 _abi.check(lib.mmuon_ns_stage(C.byref(gl.struct), it, NS_STEPS, st, _COEFFS,
                                               -0.02 * gl.alpha_scale, 0, stream), "mmuon_ns_stage")
             launch()
@@ -701,7 +724,7 @@ def stage_table(args, w):
                 loops.append(e0.elapsed_time(e1) / 20)
             ms = statistics.median(loops)
             nbytes = stage_bytes(kind, gl)
-            ex = stage_exec_flops("px" if kind == "px_apply" else kind, gl)
+            ex = stage_exec_flops(kind, gl)
             rows.append({"group": f"{gl.rows}x{gl.cols}x{gl.nblocks}", "stage": kind, "ms": round(ms, 4),
                          "alg_bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
                          "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
@@ -886,16 +909,23 @@ def traffic_summary(args):
         return [rows[i] for i in sorted(rows)]
 
     fs, ws_ = seq(fetch_csv, "FETCH_SIZE"), seq(write_csv, "WRITE_SIZE")
-    groups = [("1024x1024", 1408, 1024, 1024), ("2752x1024", 256, 1024, 2752), ("1024x2752", 128, 1024, 2752)]
+    from monarch_muon_amd import _abi
+    groups = [("1024x1024", 1408, 1024, 1024), ("2752x1024", 256, 2752, 1024), ("1024x2752", 128, 1024, 2752)]
+    # the instrumented step launches, per group, the pack and then the ops of its plan
+    plans = [_abi.ns_plan(r, c, _abi.BF16, 5) for _, _, r, c in groups]
+    total = sum(1 + len(ops) for ops in plans)
     per_group = []
-    if len(fs) >= 48 and len(fs) == len(ws_):
-        last_f, last_w = fs[-48:], ws_[-48:]
-        for g, (name, N, m, n) in enumerate(groups):
-            for j in range(1, 16):
-                k, fk = last_f[16 * g + j]
-                per_group.append({"group": name, "iteration": (j - 1) // 3, "kernel": k,
+    if len(fs) >= total and len(fs) == len(ws_):
+        last_f, last_w = fs[-total:], ws_[-total:]
+        base = 0
+        for (name, N, _, _), ops in zip(groups, plans):
+            for j, op in enumerate(ops, start=1):
+                k, fk = last_f[base + j]
+                per_group.append({"group": name, "iteration": op.iteration, "kernel": k,
                                   "read_mib_per_block": round(fk * 1024 * fscale / N / 2 ** 20, 3),
-                                  "write_mib_per_block": round(last_w[16 * g + j][1] * 1024 * wscale / N / 2 ** 20, 3)})
+                                  "write_mib_per_block": round(last_w[base + j][1] * 1024 * wscale / N / 2 ** 20,
+                                                               3)})
+            base += 1 + len(ops)
     Path(out_path).write_text(json.dumps({"calibration": {"fetch_scale": fscale, "write_scale": wscale},
                                           "kernels": kernels, "per_group": per_group}, indent=1) + "\n")
     print(json.dumps({k: round(v["bytes"] / 1e9, 3) for k, v in kernels.items()}, indent=1))
@@ -1052,8 +1082,9 @@ def main():
                 rec[3] += stage_exec_flops(kind, gl)
             stage_ms[kind] += ms
     reps = max(1, args.instrumented)
-    ns_ms = sum(stage_ms[k] for k in ("syrk", "poly", "px")) / reps
+    ns_ms = sum(stage_ms[k] for k in NS_KINDS) / reps
     ns_tf = ns_flops(w) / (ns_ms * 1e-3) / 1e12
+    ns_exec = sum(v[3] for k, v in per.items() if k.startswith("ns_")) / reps
     dominant = max((k for k in per if k.startswith("ns_")), key=lambda k: per[k][0])
     d_ms, d_n, d_fl, d_ex = per[dominant]
     d_avg = d_ms / d_n
@@ -1100,11 +1131,20 @@ def main():
                                                                   "mfma_busy", "gfx_mhz") if k in counters}}}
                         if counters else {})},
         "newton_schulz": {"ms": round(ns_ms, 3), "alg_tflop": round(ns_flops(w) / 1e12, 2),
-                          "alg_tflops": round(ns_tf, 1), "frac_peak": round(ns_tf / PEAK_BF16_TFLOPS, 4)},
+                          "alg_tflops": round(ns_tf, 1), "frac_peak": round(ns_tf / PEAK_BF16_TFLOPS, 4),
+                          "exec_tflop": round(ns_exec / 1e12, 2),
+                          "exec_tflops": round(ns_exec / (ns_ms * 1e-3) / 1e12, 1),
+                          "exec_frac_peak": round(ns_exec / (ns_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                          "forms": {f"{gl.rows}x{gl.cols}x{gl.nblocks}":
+                                    "gram" if any(op.kind == 4 for op in _ns_plan(gl, opt)) else "chain"
+                                    for gl in opt._muon_planner.groups},
+                          "note": "alg_tflop: the reference's three-product chain (2m^2(2n+m) per block and "
+                                  "iteration, symmetric products counted in full), the work every evaluation "
+                                  "order replaces; exec_tflop: the MFMA work the launched kernels execute"},
         "momentum_pack": {"ms": round(pack_ms, 3), "alg_bytes": pack_b,
                           "gbs": round(pack_b / (pack_ms * 1e-3) / 1e9, 1),
                           "frac_hbm": round(pack_b / (pack_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
-        "muon_group_ms": round(sum(stage_ms[k] for k in ("pack", "syrk", "poly", "px")) / reps, 3),
+        "muon_group_ms": round(sum(stage_ms[k] for k in ("pack",) + NS_KINDS) / reps, 3),
         "adamw_ms": round(stage_ms["adamw"] / reps, 3),
         "adamw_gbs": round(adamw_bytes(w) / (stage_ms["adamw"] / reps * 1e-3) / 1e9, 1),
         "kernels": kernels,

@@ -122,18 +122,83 @@ int mmuon_fp8_momentum_pack(const mmuon_group* g, float momentum, int32_t have_s
                             void* stream);
 
 /* Newton-Schulz over the group's stack (already packed into g->x0) followed by
-   the weight update (X ping-pongs between x0 and x1):
+   the weight update:
      X <- X / (||X||_F + 1e-7)  (norm from the packed partial sums)
      repeat iters: A = X X^T ; P = b A + c A A ; X = a X + P X
      param <- param + alpha * cast(X) (un-transposed), alpha = -lr*sqrt(r/c)
-   coeffs = {a, b, c}.  flags: MMUON_NS_NO_APPLY leaves the final X in the
-   workspace (x0 when iters is even, x1 otherwise) and does not touch params.
+   coeffs = {a, b, c}.  The launches are the ops of mmuon_ns_plan(g->rows,
+   g->cols, g->ns_dtype, iters, flags): the three-product chain (X ping-pongs
+   between x0 and x1), or for bf16 groups with np_ >= 2 mp and iters == 5 the
+   Gram form (see mmuon_ns_plan).  flags: MMUON_NS_NO_APPLY leaves the final X
+   in the workspace stack named by the plan's last op (standard chain: x0 when
+   iters is even, x1 otherwise; Gram form: x0) and does not touch params;
+   MMUON_NS_STANDARD selects the three-product chain for every group.
    Replaces membench monarch_muon.py:36-50 (_newton_schulz_batched, with the
    norm at :38-39), :164-170 (cast back, split, _foreach_add_ apply);
    pretrain monarch_muon.py:36-50,159-165. */
 #define MMUON_NS_NO_APPLY 1
+#define MMUON_NS_STANDARD 2
 int mmuon_newton_schulz_apply(const mmuon_group* g, int32_t iters, const float coeffs[3],
                               float alpha, int32_t flags, void* stream);
+
+/* One launch of a Newton-Schulz plan.  Buffers: the group's workspace stacks
+   x0, x1 (m x n), a, p (m x m), the two m x m sub-stacks of each X stack
+   (X*_S0 at its start, X*_S1 after N mp^2 elements; only when np_ >= 2 mp),
+   and the parameters.  Kinds (bf16 stacks keep symmetric m x m matrices as
+   their 256 x 256 tiles on and above the diagonal):
+     SYRK     out = s^2 in0 in0^T            (in0 an X stack)
+     POLY     out = a I + b in0 + c in0 in0
+     SYMM     out = in0 in1                  (two symmetric stacks that commute;
+                                              bf16 only)
+     PX       out = s in0 in1                (in1 an X stack, out an X stack)
+     PX_APPLY param += alpha cast(s in0 in1)  (un-transposed)
+   s = the block's 1/(||X_0||_F + 1e-7) when `scaled`, else 1. */
+enum {
+  MMUON_NSOP_SYRK = 0,
+  MMUON_NSOP_POLY = 1,
+  MMUON_NSOP_PX = 2,
+  MMUON_NSOP_PX_APPLY = 3,
+  MMUON_NSOP_SYMM = 4
+};
+enum {
+  MMUON_NSB_X0 = 0,
+  MMUON_NSB_X1 = 1,
+  MMUON_NSB_A = 2,
+  MMUON_NSB_P = 3,
+  MMUON_NSB_X0_S0 = 4,
+  MMUON_NSB_X0_S1 = 5,
+  MMUON_NSB_X1_S0 = 6,
+  MMUON_NSB_X1_S1 = 7,
+  MMUON_NSB_PARAM = 8
+};
+typedef struct mmuon_ns_op {
+  int32_t kind;       /* MMUON_NSOP_*                                   */
+  int32_t in0, in1;   /* MMUON_NSB_* operands (in1 unused by SYRK, POLY) */
+  int32_t out;        /* MMUON_NSB_* output                             */
+  int32_t scaled;     /* 1: the op applies the block's normalisation    */
+  int32_t iteration;  /* the quintic iteration the op belongs to        */
+} mmuon_ns_op;
+
+/* The launch plan of mmuon_newton_schulz_apply for a group of (rows x cols)
+   blocks: writes up to max_ops ops (none when ops is NULL) and returns their
+   number, or a negative error code.  Three-product chain: SYRK, POLY, PX per
+   iteration.  Gram form (ns_dtype BF16, np_ >= 2 mp, iters == 5, no
+   MMUON_NS_STANDARD): X_k = Q_k X_0 with Q_k a polynomial in A_0 = X_0 X_0^T, so
+     P_k = a I + b A_k + c A_k^2, Q_{k+1} = P_k Q_k, A_{k+1} = P_k (P_k A_k)
+   run on m x m matrices; X is rebuilt once (X_3 = Q_3 X_0) and the last two
+   iterations restart from A_3 = X_3 X_3^T.  Equal to the chain in exact
+   arithmetic; it replaces the m x m x n products of the other iterations by
+   m x m x m ones.  Same reference lines as mmuon_newton_schulz_apply
+   (the iteration of monarch_muon.py:43-48 re-associated). */
+int mmuon_ns_plan(int32_t rows, int32_t cols, int32_t ns_dtype, int32_t iters, int32_t flags,
+                  mmuon_ns_op* ops, int32_t max_ops);
+
+/* Run one op of a plan on group g (validates the op against the group's
+   geometry: buffer kinds, overlaps, sub-stack room).  A plan's ops run in order
+   on one stream are exactly mmuon_newton_schulz_apply; this entry exists so a
+   caller can time or inspect each launch.  Same reference lines. */
+int mmuon_ns_run_op(const mmuon_group* g, const mmuon_ns_op* op, const float coeffs[3], float alpha,
+                    void* stream);
 
 /* One stage of one Newton-Schulz iteration (stage 0 = Gram X X^T, 1 = polynomial,
    2 = X update; on the last iteration stage 2 also applies the weight update
@@ -141,9 +206,10 @@ int mmuon_newton_schulz_apply(const mmuon_group* g, int32_t iters, const float c
    P = a I + b A + c A A (the a X term rides on P's diagonal, added in fp32
    before P's bf16 rounding) and stage 2 computes X = P X; with an fp32 group it
    stores P = b A + c A A and stage 2 computes X = a X + P X.
-   mmuon_newton_schulz_apply is exactly the loop
-   over (iteration, stage); this entry exists so a caller can time each kernel
-   with its own events.  Same reference lines as mmuon_newton_schulz_apply. */
+   These are the ops of the three-product chain (the plan with
+   MMUON_NS_STANDARD), which mmuon_newton_schulz_apply runs for groups outside
+   the Gram form; this entry exists so a caller can time each kernel with its
+   own events.  Same reference lines as mmuon_newton_schulz_apply. */
 int mmuon_ns_stage(const mmuon_group* g, int32_t iteration, int32_t iters, int32_t stage,
                    const float coeffs[3], float alpha, int32_t flags, void* stream);
 

@@ -16,7 +16,11 @@ LIB_PATH = Path(os.environ.get("MMUON_LIB", Path(__file__).resolve().parent / "l
 F32, BF16, F8E4M3 = 0, 1, 2
 GROUP_ALIGNED16 = 1
 NS_NO_APPLY = 1
-ABI_VERSION = 5
+NS_STANDARD = 2
+ABI_VERSION = 6
+# Newton-Schulz plan ops (MMUON_NSOP_*) and buffers (MMUON_NSB_*)
+NSOP_SYRK, NSOP_POLY, NSOP_PX, NSOP_PX_APPLY, NSOP_SYMM = 0, 1, 2, 3, 4
+NSB_X0, NSB_X1, NSB_A, NSB_P, NSB_X0_S0, NSB_X0_S1, NSB_X1_S0, NSB_X1_S1, NSB_PARAM = range(9)
 NOALLOC_SCRATCH_FLOATS = 1 << 20
 
 _DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8E4M3}
@@ -50,6 +54,11 @@ class Group(C.Structure):
                 ("blocks", C.c_void_p), ("fp8", C.c_void_p),
                 ("x0", C.c_void_p), ("x1", C.c_void_p), ("a", C.c_void_p), ("p", C.c_void_p),
                 ("partial", C.c_void_p), ("scale", C.c_void_p), ("grad_scale", C.c_void_p)]
+
+
+class NsOp(C.Structure):
+    _fields_ = [("kind", C.c_int32), ("in0", C.c_int32), ("in1", C.c_int32), ("out", C.c_int32),
+                ("scaled", C.c_int32), ("iteration", C.c_int32)]
 
 
 class AdamWTensor(C.Structure):
@@ -102,6 +111,10 @@ SIGNATURES = {
                                             C.c_float, C.c_int32, C.c_void_p]),
     "mmuon_ns_stage": (C.c_int, [C.POINTER(Group), C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_float),
                                  C.c_float, C.c_int32, C.c_void_p]),
+    "mmuon_ns_plan": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.POINTER(NsOp),
+                                C.c_int32]),
+    "mmuon_ns_run_op": (C.c_int, [C.POINTER(Group), C.POINTER(NsOp), C.POINTER(C.c_float), C.c_float,
+                                  C.c_void_p]),
     "mmuon_adamw": (C.c_int, [C.POINTER(AdamWArgs), C.c_void_p]),
     "mmuon_adamw_fp8": (C.c_int, [C.POINTER(AdamWArgs), C.POINTER(AdamWFp8Tensor), C.c_int32,
                                   C.c_void_p]),
@@ -153,6 +166,24 @@ def stream_handle(device: torch.device) -> int:
 def ns_layout(rows: int, cols: int, ns_dtype: int, nblocks: int) -> NsLayout:
     out = NsLayout()
     check(lib().mmuon_ns_layout(rows, cols, ns_dtype, nblocks, C.byref(out)), "mmuon_ns_layout")
+    return out
+
+
+def ns_plan(rows: int, cols: int, ns_dtype: int, iters: int, flags: int = 0) -> list[NsOp]:
+    """The launch plan ``mmuon_newton_schulz_apply`` runs for a group of
+    (rows x cols) blocks (host-only: no GPU needed)."""
+    n = lib().mmuon_ns_plan(rows, cols, ns_dtype, iters, flags, None, 0)
+    check(min(n, 0), "mmuon_ns_plan")
+    ops = (NsOp * n)()
+    check(min(lib().mmuon_ns_plan(rows, cols, ns_dtype, iters, flags, ops, n), 0), "mmuon_ns_plan")
+    return list(ops)
+
+
+def ns_output_buffer(rows: int, cols: int, ns_dtype: int, iters: int, flags: int = NS_NO_APPLY) -> int:
+    """Workspace X stack (0: x0, 1: x1) holding the Newton-Schulz output of a
+    ``MMUON_NS_NO_APPLY`` run: the output of the plan's last op."""
+    out = ns_plan(rows, cols, ns_dtype, iters, flags | NS_NO_APPLY)[-1].out
+    assert out in (NSB_X0, NSB_X1)
     return out
 
 

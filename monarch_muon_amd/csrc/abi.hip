@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <string>
+#include <vector>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -129,7 +130,7 @@ extern "C" {
 
 const char* mmuon_last_error(void) { return g_err.c_str(); }
 
-int mmuon_abi_version(void) { return 5; }
+int mmuon_abi_version(void) { return 6; }
 
 int mmuon_ns_layout(int32_t rows, int32_t cols, int32_t ns_dtype, int64_t nblocks,
                     mmuon_ns_layout_t* out) {
@@ -188,10 +189,135 @@ int mmuon_fp8_momentum_pack(const mmuon_group* g, float momentum, int32_t have_s
 
 namespace {
 
-// Launch one stage of one iteration; X ping-pongs between x0 (even iterations'
-// input) and x1.
-int ns_stage(const mmuon_group* g, const Geometry& geo, int it, int iters, int stage,
-             const float coeffs[3], float alpha, int flags, hipStream_t s) {
+// ---------------------------------------------------------------------------
+// Newton-Schulz plans.  A plan is the list of stage launches of one group's
+// iterations; mmuon_newton_schulz_apply runs it, mmuon_ns_plan hands it to the
+// caller (per-launch timing, the stage tests) and mmuon_ns_run_op runs one op.
+//
+// Standard chain, per iteration: A = X X^T; P = a I + b A + c A A; X = P X
+// (the a X term on P's diagonal).  Gram form (bf16 groups with n >= 2m after
+// padding, 5 iterations): every X_k = Q_k X_0 with Q_k a polynomial in the
+// first Gram matrix A_0, so the iterations can run on m x m matrices:
+//   P_k = a I + b A_k + c A_k^2,  Q_{k+1} = P_k Q_k,  A_{k+1} = P_k (P_k A_k)
+// (all symmetric and commuting: products of polynomials in A_0).  This
+// replaces the two m x m x n products of an iteration by m x m x m ones.  In
+// bf16 the Gram recursion alone drifts on ill-conditioned blocks, so X is
+// rebuilt once, X_3 = Q_3 X_0, and the last two iterations restart from A_3 =
+// X_3 X_3^T (three Gram iterations, restart, two).  The m x m intermediates
+// beyond A and P use the idle X stack's memory (n >= 2m: two m x m stacks fit
+// in one m x n stack).
+// ---------------------------------------------------------------------------
+bool is_x(int b) { return b == MMUON_NSB_X0 || b == MMUON_NSB_X1; }
+bool is_sym(int b) {
+  return b == MMUON_NSB_A || b == MMUON_NSB_P || (b >= MMUON_NSB_X0_S0 && b <= MMUON_NSB_X1_S1);
+}
+// the X stack whose memory holds sub-stack b (or b itself), -1 for A, P
+int x_home(int b) {
+  if (b == MMUON_NSB_X0 || b == MMUON_NSB_X0_S0 || b == MMUON_NSB_X0_S1) return MMUON_NSB_X0;
+  if (b == MMUON_NSB_X1 || b == MMUON_NSB_X1_S0 || b == MMUON_NSB_X1_S1) return MMUON_NSB_X1;
+  return -1;
+}
+bool overlaps(int u, int v) {
+  if (u == v) return true;
+  const int hu = x_home(u), hv = x_home(v);
+  // a sub-stack overlaps its X stack; the two sub-stacks of one X stack do not
+  return hu >= 0 && hu == hv && (is_x(u) || is_x(v));
+}
+
+bool gram_eligible(const Geometry& geo, int ns_dtype, int iters, int flags) {
+  return ns_dtype == MMUON_BF16 && !(flags & MMUON_NS_STANDARD) && iters == 5 &&
+         int64_t(geo.np_) >= 2 * int64_t(geo.mp);
+}
+
+void build_plan(const Geometry& geo, int ns_dtype, int iters, int flags, std::vector<mmuon_ns_op>& ops) {
+  ops.clear();
+  const bool apply = !(flags & MMUON_NS_NO_APPLY);
+  auto op = [&](int kind, int in0, int in1, int out, int scaled, int it) {
+    ops.push_back(mmuon_ns_op{kind, in0, in1, out, scaled, it});
+  };
+  if (!gram_eligible(geo, ns_dtype, iters, flags)) {
+    for (int it = 0; it < iters; ++it) {
+      const int cur = (it & 1) ? MMUON_NSB_X1 : MMUON_NSB_X0;
+      const int nxt = (it & 1) ? MMUON_NSB_X0 : MMUON_NSB_X1;
+      op(MMUON_NSOP_SYRK, cur, -1, MMUON_NSB_A, it == 0, it);
+      op(MMUON_NSOP_POLY, MMUON_NSB_A, -1, MMUON_NSB_P, 0, it);
+      if (apply && it + 1 == iters) op(MMUON_NSOP_PX_APPLY, MMUON_NSB_P, cur, MMUON_NSB_PARAM, it == 0, it);
+      else op(MMUON_NSOP_PX, MMUON_NSB_P, cur, nxt, it == 0, it);
+    }
+    return;
+  }
+  enum { X0 = MMUON_NSB_X0, X1 = MMUON_NSB_X1, A = MMUON_NSB_A, P = MMUON_NSB_P,
+         X0S0 = MMUON_NSB_X0_S0, X1S0 = MMUON_NSB_X1_S0, X1S1 = MMUON_NSB_X1_S1 };
+  const int SYRK = MMUON_NSOP_SYRK, POLY = MMUON_NSOP_POLY, SYMM = MMUON_NSOP_SYMM;
+  // iteration 0 (X_0 in x0, scaled by s): A_0, P_0 = Q_1, A_1 = P_0 (P_0 A_0)
+  op(SYRK, X0, -1, A, 1, 0);
+  op(POLY, A, -1, P, 0, 0);
+  op(SYMM, P, A, X1S0, 0, 0);
+  op(SYMM, P, X1S0, A, 0, 0);
+  // iteration 1: P_1, Q_2 = P_1 Q_1, A_2 = P_1 (P_1 A_1)
+  op(POLY, A, -1, X1S0, 0, 1);
+  op(SYMM, X1S0, P, X1S1, 0, 1);
+  op(SYMM, X1S0, A, P, 0, 1);
+  op(SYMM, X1S0, P, A, 0, 1);
+  // iteration 2: P_2, Q_3 = P_2 Q_2, restart X_3 = s Q_3 X_0 (into x1)
+  op(POLY, A, -1, P, 0, 2);
+  op(SYMM, P, X1S1, A, 0, 2);
+  op(MMUON_NSOP_PX, A, X0, X1, 1, 2);
+  // iteration 3: A_3 = X_3 X_3^T, P_3 = Q_4, A_4 = P_3 (P_3 A_3)
+  op(SYRK, X1, -1, A, 0, 3);
+  op(POLY, A, -1, P, 0, 3);
+  op(SYMM, P, A, X0S0, 0, 3);
+  op(SYMM, P, X0S0, A, 0, 3);
+  // iteration 4: P_4, Q_5 = P_4 Q_4, X_5 = Q_5 X_3 (applied, or into x0)
+  op(POLY, A, -1, X0S0, 0, 4);
+  op(SYMM, X0S0, P, A, 0, 4);
+  if (apply) op(MMUON_NSOP_PX_APPLY, A, X1, MMUON_NSB_PARAM, 0, 4);
+  else op(MMUON_NSOP_PX, A, X1, X0, 0, 4);
+}
+
+int check_op(const Geometry& geo, int ns_dtype, const mmuon_ns_op* op) {
+  if (op == nullptr) return fail(MMUON_EINVAL, "null Newton-Schulz op");
+  const int k = op->kind, i0 = op->in0, i1 = op->in1, o = op->out;
+  bool ok;
+  switch (k) {
+    case MMUON_NSOP_SYRK: ok = is_x(i0) && is_sym(o); break;
+    case MMUON_NSOP_POLY: ok = is_sym(i0) && is_sym(o); break;
+    case MMUON_NSOP_SYMM: ok = is_sym(i0) && is_sym(i1) && is_sym(o); break;
+    case MMUON_NSOP_PX: ok = is_sym(i0) && is_x(i1) && is_x(o); break;
+    case MMUON_NSOP_PX_APPLY: ok = is_sym(i0) && is_x(i1) && o == MMUON_NSB_PARAM; break;
+    default: return fail(MMUON_EINVAL, "unknown Newton-Schulz op kind %d", k);
+  }
+  if (!ok) return fail(MMUON_EINVAL, "op kind %d: operand or output buffer of the wrong kind (%d, %d -> %d)", k, i0,
+                       i1, o);
+  const bool two = k == MMUON_NSOP_SYMM || k == MMUON_NSOP_PX || k == MMUON_NSOP_PX_APPLY;
+  if (overlaps(o, i0) || (two && overlaps(o, i1)))
+    return fail(MMUON_EINVAL, "op kind %d: output %d overlaps an operand", k, o);
+  for (int b : {i0, two ? i1 : i0, o})
+    if (b >= MMUON_NSB_X0_S0 && b <= MMUON_NSB_X1_S1 && int64_t(geo.np_) < 2 * int64_t(geo.mp))
+      return fail(MMUON_EINVAL, "sub-stacks of an X stack need np >= 2 mp (mp %d, np %d)", geo.mp, geo.np_);
+  if (k == MMUON_NSOP_SYMM && ns_dtype != MMUON_BF16)
+    return fail(MMUON_EINVAL, "the symmetric product runs on bf16 groups only");
+  return MMUON_OK;
+}
+
+void* buf_ptr(const mmuon_group* g, const Geometry& geo, int b) {
+  const int64_t sub = int64_t(g->nblocks) * geo.mp * geo.mp * dtype_size(g->ns_dtype);
+  char* x0 = static_cast<char*>(g->x0);
+  char* x1 = static_cast<char*>(g->x1);
+  switch (b) {
+    case MMUON_NSB_X0: case MMUON_NSB_X0_S0: return x0;
+    case MMUON_NSB_X1: case MMUON_NSB_X1_S0: return x1;
+    case MMUON_NSB_X0_S1: return x0 + sub;
+    case MMUON_NSB_X1_S1: return x1 + sub;
+    case MMUON_NSB_A: return g->a;
+    case MMUON_NSB_P: return g->p;
+  }
+  return nullptr;
+}
+
+int run_op(const mmuon_group* g, const Geometry& geo, const mmuon_ns_op& op, const float coeffs[3], float alpha,
+           hipStream_t s) {
+  if (int rc = check_op(geo, g->ns_dtype, &op)) return rc;
   mmuon::NsArgs a{};
   a.blocks = g->blocks;
   a.N = g->nblocks;
@@ -206,37 +332,34 @@ int ns_stage(const mmuon_group* g, const Geometry& geo, int it, int iters, int s
   a.alpha = alpha;
   a.transposed = geo.transposed ? 1 : 0;
   a.vec = (g->flags & MMUON_GROUP_ALIGNED16) ? 1 : 0;
-  void* cur = (it & 1) ? g->x1 : g->x0;
-  void* nxt = (it & 1) ? g->x0 : g->x1;
-  const float* sc = it == 0 ? g->scale : nullptr;
-  int kstage = stage;
-  switch (stage) {
-    case 0:
+  const float* sc = op.scaled ? g->scale : nullptr;
+  int kstage = 0;
+  switch (op.kind) {
+    case MMUON_NSOP_SYRK:
       a.scale = sc;
-      a.x_in = cur;
-      a.out = g->a;
+      a.x_in = buf_ptr(g, geo, op.in0);
       kstage = mmuon::NS_SYRK;
       break;
-    case 1:
-      a.a_in = g->a;
-      a.out = g->p;
+    case MMUON_NSOP_POLY:
+      a.a_in = buf_ptr(g, geo, op.in0);
       kstage = mmuon::NS_POLY;
       break;
-    case 2: {
-      a.scale = sc;
-      a.a_in = g->p;
-      a.x_in = cur;
-      a.out = nxt;
-      const bool apply = !(flags & MMUON_NS_NO_APPLY) && it + 1 == iters;
-      kstage = apply ? mmuon::NS_PX_APPLY : mmuon::NS_PX;
+    case MMUON_NSOP_SYMM:
+      a.a_in = buf_ptr(g, geo, op.in0);
+      a.b_in = buf_ptr(g, geo, op.in1);
+      kstage = mmuon::NS_SYMM;
       break;
-    }
-    default:
-      return fail(MMUON_EINVAL, "stage must be 0, 1 or 2 (got %d)", stage);
+    default:  // PX, PX_APPLY
+      a.scale = sc;
+      a.a_in = buf_ptr(g, geo, op.in0);
+      a.x_in = buf_ptr(g, geo, op.in1);
+      kstage = op.kind == MMUON_NSOP_PX ? mmuon::NS_PX : mmuon::NS_PX_APPLY;
+      break;
   }
+  a.out = op.out == MMUON_NSB_PARAM ? nullptr : buf_ptr(g, geo, op.out);
   if (mmuon::launch_ns_stage(a, kstage, g->ns_dtype, g->param_dtype, s))
-    return fail(MMUON_EINVAL, "no Newton-Schulz kernel for ns dtype %d / param dtype %d", g->ns_dtype,
-                g->param_dtype);
+    return fail(MMUON_EINVAL, "no Newton-Schulz kernel for op %d, ns dtype %d / param dtype %d", op.kind,
+                g->ns_dtype, g->param_dtype);
   return MMUON_OK;
 }
 
@@ -251,14 +374,39 @@ int check_ns(const mmuon_group* g, Geometry& geo, int iters, const float* coeffs
 
 extern "C" {
 
+int mmuon_ns_plan(int32_t rows, int32_t cols, int32_t ns_dtype, int32_t iters, int32_t flags, mmuon_ns_op* ops,
+                  int32_t max_ops) {
+  Geometry geo;
+  if (int rc = geometry(rows, cols, ns_dtype, geo)) return rc;
+  if (iters < 1 || iters > 64) return fail(MMUON_EINVAL, "iters must be in [1, 64] (got %d)", iters);
+  std::vector<mmuon_ns_op> plan;
+  build_plan(geo, ns_dtype, iters, flags, plan);
+  const int n = int(plan.size());
+  if (ops != nullptr) {
+    if (max_ops < n) return fail(MMUON_ERANGE, "plan has %d ops, room for %d", n, max_ops);
+    std::copy(plan.begin(), plan.end(), ops);
+  }
+  return n;
+}
+
+int mmuon_ns_run_op(const mmuon_group* g, const mmuon_ns_op* op, const float coeffs[3], float alpha,
+                    void* stream) {
+  Geometry geo;
+  if (int rc = check_ns(g, geo, 1, coeffs)) return rc;
+  if (op == nullptr) return fail(MMUON_EINVAL, "null Newton-Schulz op");
+  if (int rc = run_op(g, geo, *op, coeffs, alpha, static_cast<hipStream_t>(stream))) return rc;
+  return check_launch("mmuon_ns_run_op");
+}
+
 int mmuon_newton_schulz_apply(const mmuon_group* g, int32_t iters, const float coeffs[3], float alpha,
                               int32_t flags, void* stream) {
   Geometry geo;
   if (int rc = check_ns(g, geo, iters, coeffs)) return rc;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  for (int it = 0; it < iters; ++it)
-    for (int st = 0; st < 3; ++st)
-      if (int rc = ns_stage(g, geo, it, iters, st, coeffs, alpha, flags, s)) return rc;
+  std::vector<mmuon_ns_op> plan;
+  build_plan(geo, g->ns_dtype, iters, flags, plan);
+  for (const mmuon_ns_op& op : plan)
+    if (int rc = run_op(g, geo, op, coeffs, alpha, s)) return rc;
   return check_launch("mmuon_newton_schulz_apply");
 }
 
@@ -268,7 +416,10 @@ int mmuon_ns_stage(const mmuon_group* g, int32_t iteration, int32_t iters, int32
   if (int rc = check_ns(g, geo, iters, coeffs)) return rc;
   if (iteration < 0 || iteration >= iters)
     return fail(MMUON_EINVAL, "iteration %d outside [0, %d)", iteration, iters);
-  if (int rc = ns_stage(g, geo, iteration, iters, stage, coeffs, alpha, flags, static_cast<hipStream_t>(stream)))
+  if (stage < 0 || stage > 2) return fail(MMUON_EINVAL, "stage must be 0, 1 or 2 (got %d)", stage);
+  std::vector<mmuon_ns_op> plan;
+  build_plan(geo, g->ns_dtype, iters, flags | MMUON_NS_STANDARD, plan);
+  if (int rc = run_op(g, geo, plan[size_t(3 * iteration + stage)], coeffs, alpha, static_cast<hipStream_t>(stream)))
     return rc;
   return check_launch("mmuon_ns_stage");
 }

@@ -28,11 +28,12 @@ void launch_block_scale(const float* partial, int nparts, float* scale, int N, b
                         hipStream_t s);
 
 // Newton-Schulz stage kernels -------------------------------------------------
-enum NsStage { NS_SYRK = 0, NS_POLY = 1, NS_PX = 2, NS_PX_APPLY = 3 };
+enum NsStage { NS_SYRK = 0, NS_POLY = 1, NS_PX = 2, NS_PX_APPLY = 3, NS_SYMM = 4 };
 
 struct NsArgs {
   const void* x_in;   // X stack, N x (mp x np)
   const void* a_in;   // Gram / polynomial stack, N x (mp x mp)
+  const void* b_in;   // SYMM: the column operand, a second symmetric N x (mp x mp) stack
   void* out;          // stage output
   const float* scale; // per-block 1/(||X||+eps) for the first iteration, else null
   const mmuon_block_ref* blocks;  // apply stage: parameter pointers

@@ -389,11 +389,12 @@ __device__ __forceinline__ void mainloop_run(const uint16_t* rsrc_k, const uint1
 // kt < thr are T (OP_SPLIT); pstride: elements per panel.  ident_v: the identity
 // scalar; diag: K index of the tile's first column (IDENT_COL).
 // sym_diag (workgroup-uniform): a diagonal tile of a symmetric product, whose
-// row and column operands are the same rows (loaded once, Pipe SHARED) and
-// whose work is dealt by diag_plan.  idle (wave-uniform, full tiles only): the
-// wave's window holds only zero padding columns; it issues its share of the
-// direct loads and leaves its accumulators zero.
-template <int RK, int CK, int IDENT = IDENT_NONE>
+// work is dealt by diag_plan; SHARE: its row and column operands are the same
+// rows (SYRK, POLY: loaded once, Pipe SHARED), else two stacks' bands of the
+// same rows (SYMM).  idle (wave-uniform, full tiles only): the wave's window
+// holds only zero padding columns; it issues its share of the direct loads and
+// leaves its accumulators zero.
+template <int RK, int CK, int IDENT = IDENT_NONE, bool SHARE = true>
 __device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t* rsrc_t, int thr_r,
                                          const uint16_t* csrc_k, const uint16_t* csrc_t, int thr_c,
                                          int64_t pstride, int KT, uint16_t* lds, f32x16 (&acc)[TMI][TMJ],
@@ -406,10 +407,10 @@ __device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t*
                                         ident_v, diag, plan.vwm, plan.vwn)
   if (!sym_diag && idle) MMUON_RUN(0, false);
   else if (!sym_diag) MMUON_RUN(MASK_FULL, false);
-  else if (plan.mask == MASK_FULL) MMUON_RUN(MASK_FULL, true);
-  else if (plan.mask == MASK_UPPER) MMUON_RUN(MASK_UPPER, true);
-  else if (plan.mask == MASK_LAST) MMUON_RUN(MASK_LAST, true);
-  else MMUON_RUN(MASK_FIRST6, true);
+  else if (plan.mask == MASK_FULL) MMUON_RUN(MASK_FULL, SHARE);
+  else if (plan.mask == MASK_UPPER) MMUON_RUN(MASK_UPPER, SHARE);
+  else if (plan.mask == MASK_LAST) MMUON_RUN(MASK_LAST, SHARE);
+  else MMUON_RUN(MASK_FIRST6, SHARE);
 #undef MMUON_RUN
 }
 
@@ -418,8 +419,11 @@ __device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t*
 // j = 64 wn + 32 tj + lane%32 and rows i = 128 wm + 32 ti + 8 qg + 4 (lane/32) + e,
 // (wm, wn) the wave's window.  diag: a diagonal tile of a symmetric product
 // computed by diag_plan; every computed tile above the diagonal also fills its
-// mirror below it, T[i][j] = D[i][j]; and its diagonal entries i = j < dlim get
-// dadd added (in fp32, before the rounding).
+// mirror below it, T[i][j] = D[i][j], and so does the upper triangle of each
+// 32 x 32 tile on the diagonal (written after, and so replacing, the values the
+// lane pairs computed below it: equal bits when both operands are one
+// symmetric matrix, rounding-level apart for SYMM's two commuting ones); its
+// diagonal entries i = j < dlim get dadd added (in fp32, before the rounding).
 __device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI][TMJ], float f,
                                            bool diag = false, float dadd = 0.f, int dlim = 0) {
   const int tid = fresh_tid();
@@ -451,14 +455,15 @@ __device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI]
         const int col = wm * WM + i * 32 + qg * 8 + (lane >> 5) * 4;
         *reinterpret_cast<uint2*>(stage + tile_off(row, col)) = make_uint2(f2bf2(v[0], v[1]), f2bf2(v[2], v[3]));
       }
-      if (diag && C > R) {
+      if (diag && C >= R) {
 #pragma unroll
         for (int qg = 0; qg < 4; ++qg)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int row = wm * WM + i * 32 + qg * 8 + (lane >> 5) * 4 + e;
             const int col = wn * WN + j * 32 + (lane & 31);
-            *reinterpret_cast<uint16_t*>(stage + tile_off(row, col)) = f2bf(f * acc[i][j][qg * 4 + e]);
+            if (C > R || row < col)
+              *reinterpret_cast<uint16_t*>(stage + tile_off(row, col)) = f2bf(f * acc[i][j][qg * 4 + e]);
           }
       }
     }
@@ -511,11 +516,13 @@ __device__ __forceinline__ void stage_cols(const char* stage, Fn&& fn) {
 }
 
 // ---------------------------------------------------------------------------
-// SYRK / POLY: symmetric m x m outputs of which only the 256 x 256 tiles on and
-// above the diagonal are computed and stored (tile ti x tc, tc >= ti; a
-// diagonal tile in full).  SYRK reads X (K form); POLY reads the stored upper
-// tiles of A (operand band R: T form left of its diagonal block, K form from
-// there on).
+// SYRK / POLY / SYMM: symmetric m x m outputs of which only the 256 x 256
+// tiles on and above the diagonal are computed and stored (tile ti x tc,
+// tc >= ti; a diagonal tile in full).  SYRK reads X (K form); POLY reads the
+// stored upper tiles of A (operand band R: T form left of its diagonal block,
+// K form from there on); SYMM (C = S1 S2 of two symmetric stacks that commute,
+// as polynomials in one Gram matrix do, so C is symmetric) reads its row band
+// from S1 and its column band from S2 in the same way.
 // ---------------------------------------------------------------------------
 static_assert(BM == BN, "square tiles: a symmetric tile is either diagonal or strictly upper");
 template <int STAGE>
@@ -536,6 +543,8 @@ __device__ __forceinline__ void sym_work(const NsArgs& a, uint16_t* lds, int v) 
     src = static_cast<const uint16_t*>(a.a_in) + int64_t(b) * a.mp * a.mp;
     K = a.mp;
   }
+  // SYMM: the column operand's stack (POLY: the row operand's own)
+  const uint16_t* src2 = STAGE == NS_SYMM ? static_cast<const uint16_t*>(a.b_in) + int64_t(b) * a.mp * a.mp : src;
   const int64_t pstride = int64_t(a.mp) * PANEL;
   const int r0 = ti * BM, c0 = tc * BN;
   // on a diagonal tile only the 32 x 32 tiles on or above the diagonal are
@@ -545,10 +554,14 @@ __device__ __forceinline__ void sym_work(const NsArgs& a, uint16_t* lds, int v) 
   if (STAGE == NS_SYRK)
     mainloop<OP_K, OP_K>(src + r0 * PANEL, nullptr, 0, src + c0 * PANEL, nullptr, 0, pstride, K / BK, lds, acc,
                          0.f, 0, diag);
-  else  // acc = A A + (b/c) A, so P = c acc + a I = a I + b A + c A A
+  else if (STAGE == NS_POLY)  // acc = A A + (b/c) A, so P = c acc + a I = a I + b A + c A A
     mainloop<OP_SPLIT, OP_SPLIT, IDENT_COL>(src + r0 * PANEL, src + (r0 / PANEL) * pstride, r0 / BK,
                                             src + c0 * PANEL, src + (c0 / PANEL) * pstride, c0 / BK,
                                             pstride, K / BK, lds, acc, a.cb / a.cc, c0, diag);
+  else  // SYMM: acc = S1 S2; a diagonal tile loads both operands' bands
+    mainloop<OP_SPLIT, OP_SPLIT, IDENT_NONE, false>(src + r0 * PANEL, src + (r0 / PANEL) * pstride, r0 / BK,
+                                                    src2 + c0 * PANEL, src2 + (c0 / PANEL) * pstride, c0 / BK,
+                                                    pstride, K / BK, lds, acc, 0.f, 0, diag);
 
   float f = STAGE == NS_POLY ? a.cc : 1.f;  // SYRK: s^2 on the first iteration
   if (STAGE == NS_SYRK && a.scale != nullptr) {
@@ -903,7 +916,7 @@ __global__ __launch_bounds__(256) void ns_f32(NsArgs a) {
 template <int STAGE, class TP>
 void launch_bf16(const NsArgs& a, hipStream_t s) {
   const int nb8 = 8 * ((a.N + 7) / 8);
-  if constexpr (STAGE == NS_SYRK || STAGE == NS_POLY) {
+  if constexpr (STAGE == NS_SYRK || STAGE == NS_POLY || STAGE == NS_SYMM) {
     const int nt = a.mp / BM;
     const int nc = a.mp / BN;
     const int total = nb8 * (nt * nc - R_SYM * nt * (nt - 1) / 2);
@@ -938,6 +951,7 @@ int launch_ns_stage(const NsArgs& a, int stage, int ns_dtype, int param_dtype, h
     switch (stage) {
       case NS_SYRK: launch_bf16<NS_SYRK, BF16T>(a, s); return 0;
       case NS_POLY: launch_bf16<NS_POLY, BF16T>(a, s); return 0;
+      case NS_SYMM: launch_bf16<NS_SYMM, BF16T>(a, s); return 0;
       case NS_PX: launch_bf16<NS_PX, BF16T>(a, s); return 0;
       case NS_PX_APPLY:
         if (param_dtype == MMUON_BF16) launch_bf16<NS_PX_APPLY, BF16T>(a, s);

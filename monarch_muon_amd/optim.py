@@ -10,6 +10,14 @@ on the GPU through ``libmmuon.so``; parameters must live on a ROCm device.
 ``torch.bfloat16`` (default) -- the membench copy: each same-shape stack is
 cast to bf16 for Newton-Schulz (the published-step-time variant);
 ``None`` -- the pretrain copy: Newton-Schulz in the momentum dtype.
+
+``ns_form`` selects how bf16 Newton-Schulz is evaluated for rectangular groups:
+``"auto"`` (default) -- the Gram form (five iterations on m x m matrices with
+one rebuild of X, ``mmuon_ns_plan``) for bf16 groups whose padded long side is
+at least twice the short side, the three-product chain elsewhere;
+``"standard"`` -- the three-product chain ``A = XX^T, P = aI + bA + cA^2,
+X = PX`` for every group.  Both equal the reference's iteration in exact
+arithmetic.
 """
 from __future__ import annotations
 
@@ -38,7 +46,8 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
 
     def __init__(self, muon_params, adamw_params, *, lr: float = 5e-3, momentum: float = 0.95,
                  adamw_betas: tuple = (0.9, 0.95), adamw_weight_decay: float = 0.1,
-                 adamw_eps: float = 1e-8, ns_dtype: torch.dtype | None = torch.bfloat16):
+                 adamw_eps: float = 1e-8, ns_dtype: torch.dtype | None = torch.bfloat16,
+                 ns_form: str = "auto"):
         muon_params = list(muon_params)
         adamw_params = list(adamw_params)
         defaults = dict(lr=lr)
@@ -51,6 +60,10 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
         if ns_dtype not in (torch.bfloat16, torch.float32, None):
             raise ValueError("ns_dtype must be torch.bfloat16, torch.float32 or None")
         self.ns_dtype = ns_dtype
+        if ns_form not in ("auto", "standard"):
+            raise ValueError('ns_form must be "auto" or "standard"')
+        self.ns_form = ns_form
+        self._ns_flags = _abi.NS_STANDARD if ns_form == "standard" else 0
         self._muon_planner = MuonPlanner()
         self._adam_planner = AdamPlanner()
         self._norm_planner = NormPlanner()
@@ -164,7 +177,7 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
             self._mark_end(ev)
             ev = self._mark("ns", gl)
             _abi.check(lib.mmuon_newton_schulz_apply(C.byref(gl.struct), NS_STEPS, _COEFFS,
-                                                     -lr * gl.alpha_scale, 0, stream),
+                                                     -lr * gl.alpha_scale, self._ns_flags, stream),
                        "mmuon_newton_schulz_apply")
             self._mark_end(ev)
 
@@ -351,7 +364,7 @@ class CoatStateMonarchMuon(MonarchMuonOptimizer):
             self._mark_end(ev)
             ev = self._mark("ns", gl)
             _abi.check(lib.mmuon_newton_schulz_apply(C.byref(gl.struct), NS_STEPS, _COEFFS,
-                                                     -lr * gl.alpha_scale, 0, stream),
+                                                     -lr * gl.alpha_scale, self._ns_flags, stream),
                        "mmuon_newton_schulz_apply")
             self._mark_end(ev)
 

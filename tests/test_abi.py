@@ -33,7 +33,8 @@ def test_struct_layouts_match_header(tmp_path):
                "mmuon_ns_layout_t": _abi.NsLayout, "mmuon_group": _abi.Group,
                "mmuon_adamw_tensor": _abi.AdamWTensor, "mmuon_adamw_args": _abi.AdamWArgs,
                "mmuon_adamw_fp8_tensor": _abi.AdamWFp8Tensor, "mmuon_grad_tensor": _abi.GradTensor,
-               "mmuon_grad_norm_args": _abi.GradNormArgs, "mmuon_butterfly_args": _abi.ButterflyArgs}
+               "mmuon_grad_norm_args": _abi.GradNormArgs, "mmuon_butterfly_args": _abi.ButterflyArgs,
+               "mmuon_ns_op": _abi.NsOp}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
     for cname, py in structs.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')

@@ -69,7 +69,7 @@ def test_full_6p89b_step():
         # block order inside the group: member parameters in order, blocks in order
         owner = [(i, k) for i in gl.members for k in range(params[i].shape[0])]
         assert len(owner) == gl.nblocks
-        x = gl.ws.x_view(1, torch.bfloat16, gl.nblocks)   # 5 iterations end in x1
+        x = gl.ws.x_view(_abi.ns_output_buffer(gl.rows, gl.cols, lay.ns_dtype, 5), torch.bfloat16, gl.nblocks)
         for blk in (0, gl.nblocks - 1):
             u = x[blk, :lay.m, :lay.n].float()
             ns_out[owner[blk]] = (u.t() if gl.transposed else u).contiguous()

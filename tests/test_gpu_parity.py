@@ -41,9 +41,10 @@ NS_SHAPES = [(4, 256, 256), (2, 512, 1368), (2, 1376, 512), (2, 1024, 1024), (1,
              (2, 96, 136), (2, 136, 96), (3, 64, 64)]
 
 
-def run_ns_only(g: torch.Tensor, ns_dtype) -> torch.Tensor:
+def run_ns_only(g: torch.Tensor, ns_dtype, flags: int = 0) -> torch.Tensor:
     """Newton-Schulz of the stack ``g`` through the library: pack with momentum 0
-    (buf <- 0*buf + g = g), then the NS chain without the apply."""
+    (buf <- 0*buf + g = g), then the NS plan without the apply (``flags``:
+    ``NS_STANDARD`` for the three-product chain on every group)."""
     p = torch.zeros_like(g, dtype=torch.bfloat16 if ns_dtype == torch.bfloat16 else torch.float32)
     buf = torch.zeros_like(g, dtype=torch.float32)
     grad = g.to(p.dtype)
@@ -53,26 +54,68 @@ def run_ns_only(g: torch.Tensor, ns_dtype) -> torch.Tensor:
     stream = _abi.stream_handle(DEV)
     _abi.check(lib.mmuon_momentum_pack(C.byref(gl.struct), 0.0, stream), "pack")
     coeffs = (C.c_float * 3)(*NS_COEFFS)
-    _abi.check(lib.mmuon_newton_schulz_apply(C.byref(gl.struct), 5, coeffs, 0.0, _abi.NS_NO_APPLY, stream), "ns")
+    _abi.check(lib.mmuon_newton_schulz_apply(C.byref(gl.struct), 5, coeffs, 0.0, _abi.NS_NO_APPLY | flags,
+                                             stream), "ns")
     torch.cuda.synchronize()
     lay = gl.ws.layout
-    x = gl.ws.x_view(1, torch.bfloat16 if lay.ns_dtype == _abi.BF16 else torch.float32, gl.nblocks)
+    out = _abi.ns_output_buffer(gl.rows, gl.cols, lay.ns_dtype, 5, flags)
+    x = gl.ws.x_view(out, torch.bfloat16 if lay.ns_dtype == _abi.BF16 else torch.float32, gl.nblocks)
     x = x[:, :lay.m, :lay.n].float().cpu()
     return x.transpose(1, 2) if gl.transposed else x
 
 
+@pytest.mark.parametrize("form", ["auto", "standard"])
 @pytest.mark.parametrize("shape", NS_SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_ns_bf16_against_fp64_truth_and_reference(shape):
+def test_ns_bf16_against_fp64_truth_and_reference(shape, form):
+    """Both evaluation orders (the Gram form runs on the rectangular shapes with
+    a long side at least twice the short one after padding) against fp64."""
     gen = torch.Generator().manual_seed(11)
     g = (torch.randn(shape, generator=gen) * 1e-3).to(DEV)
-    ours = run_ns_only(g, torch.bfloat16)
+    ours = run_ns_only(g, torch.bfloat16, _abi.NS_STANDARD if form == "standard" else 0)
     ref_bf16 = newton_schulz_batched(g.cpu().to(torch.bfloat16)).float()
     truth = ns_fp64(g.cpu().to(torch.bfloat16).double())
     e_ours = rel_fro(ours, truth)
     e_ref = rel_fro(ref_bf16, truth)
-    print(f"NS {shape}: ours vs fp64 {e_ours.max():.4f}, reference-bf16 vs fp64 {e_ref.max():.4f}")
+    print(f"NS {shape} {form}: ours vs fp64 {e_ours.max():.4f}, reference-bf16 vs fp64 {e_ref.max():.4f}")
     assert torch.all(e_ours <= 1.5 * e_ref + 2e-3), (e_ours, e_ref)
     assert torch.all(rel_fro(ours, ref_bf16) <= 0.08)
+
+
+def _spectrum_stack(m, n, spectra, seed):
+    """One (m x n) block per singular-value profile: U diag(s) V^T with random
+    orthonormal U, V (fp64, rounded to fp32)."""
+    gen = torch.Generator().manual_seed(seed)
+    out = []
+    for sv in spectra:
+        u, _ = torch.linalg.qr(torch.randn(m, m, generator=gen, dtype=torch.float64))
+        v, _ = torch.linalg.qr(torch.randn(n, m, generator=gen, dtype=torch.float64))
+        out.append(((u * sv) @ v.T).float())
+    return torch.stack(out)
+
+
+@pytest.mark.parametrize("shape", [(1024, 2752), (512, 1376), (2752, 1024)], ids=lambda s: "x".join(map(str, s)))
+def test_ns_bf16_ill_conditioned_blocks(shape):
+    """Blocks whose singular values span decades (where a Gram recursion in bf16
+    without the rebuild of X drifts by up to 1.3 in relative Frobenius error):
+    both evaluation orders stay within 1.5x the reference's own bf16 error."""
+    r, c = shape
+    m, n = min(r, c), max(r, c)
+    d = torch.float64
+    spectra = [torch.logspace(0, -3, m, dtype=d), torch.logspace(0, -5, m, dtype=d),
+               torch.cat([torch.logspace(0, -1, 16, dtype=d), torch.full((m - 16,), 1e-3, dtype=d)]),
+               torch.cat([torch.ones(1, dtype=d), torch.full((m - 1,), 1e-4, dtype=d)])]
+    g = _spectrum_stack(m, n, spectra, seed=21)
+    if r > c:
+        g = g.transpose(1, 2).contiguous()
+    ref_bf16 = newton_schulz_batched(g.to(torch.bfloat16)).float()
+    truth = ns_fp64(g.to(torch.bfloat16).double())
+    e_ref = rel_fro(ref_bf16, truth)
+    for flags in (0, _abi.NS_STANDARD):
+        ours = run_ns_only(g.to(DEV), torch.bfloat16, flags)
+        e_ours = rel_fro(ours, truth)
+        print(f"NS {shape} flags {flags}: ours {[round(float(e), 4) for e in e_ours]}, "
+              f"reference {[round(float(e), 4) for e in e_ref]}")
+        assert torch.all(e_ours <= 1.5 * e_ref + 2e-3), (flags, e_ours, e_ref)
 
 
 @pytest.mark.parametrize("shape", [(4, 256, 256), (2, 256, 688), (2, 688, 256), (2, 96, 136)],
@@ -272,7 +315,8 @@ def test_6p89b_layer_newton_schulz_output_against_fp64():
                    "ns")
         torch.cuda.synchronize()
         lay = gl.ws.layout
-        x = gl.ws.x_view(1, torch.bfloat16, gl.nblocks)[:, :lay.m, :lay.n].float().cpu()
+        out = _abi.ns_output_buffer(gl.rows, gl.cols, lay.ns_dtype, 5)
+        x = gl.ws.x_view(out, torch.bfloat16, gl.nblocks)[:, :lay.m, :lay.n].float().cpu()
         ours = x.transpose(1, 2) if gl.transposed else x
         stack = torch.cat([ref_bufs[i] for i in gl.members]).to(torch.bfloat16)
         sel = list(range(0, gl.nblocks, 4)) if gl.rows == gl.cols else list(range(gl.nblocks))

@@ -56,7 +56,8 @@ def _ns_outputs(params, grads, bufs):
         _abi.check(lib.mmuon_newton_schulz_apply(C.byref(gl.struct), 5, coeffs, 0.0, _abi.NS_NO_APPLY, stream), "ns")
         lay = gl.ws.layout
         per = lay.mp * lay.np_
-        stack = gl.ws.x1.view(torch.bfloat16)[: gl.nblocks * per].view(gl.nblocks, per)  # 5 iterations end in x1
+        xs = gl.ws.x1 if _abi.ns_output_buffer(gl.rows, gl.cols, lay.ns_dtype, 5) == _abi.NSB_X1 else gl.ws.x0
+        stack = xs.view(torch.bfloat16)[: gl.nblocks * per].view(gl.nblocks, per)
         out[(gl.rows, gl.cols)] = (list(gl.members), stack.clone())
     torch.cuda.synchronize()
     planner.release()

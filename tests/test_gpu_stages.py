@@ -8,6 +8,9 @@ isolation (the end-to-end chain is covered in test_gpu_parity.py):
   POLY  P  = a I + b A + c A A  (A's lower tiles are the transposes of its upper ones;
                                  a only on the diagonal of the m valid rows)
   PX    X' = s P X
+  SYMM  C  = S1 S2              (two symmetric stacks; upper tiles stored; run through
+                                 mmuon_ns_run_op into the sub-stacks of x1, on the
+                                 shapes whose X stack holds two m x m stacks)
 
 Bar: |stage - fp64| <= 2^-8 * max|fp64| per block (one bf16 step at the largest
 entry; bf16 output rounding is at most half of that).  Diagonal 256 x 256 tiles
@@ -111,3 +114,40 @@ def test_stage_outputs_against_fp64_products(shape):
     # the zero padding stays zero through every stage
     for pad in (got[:, lay.m:, :], got[:, :, lay.n:]):
         assert pad.numel() == 0 or float(pad.abs().max()) == 0.0
+
+    if np_ < 2 * mp:
+        return
+    # SYMM (the Gram form's product of two commuting symmetric stacks): P A into
+    # the first m x m sub-stack of x1, A P into the second (its offset: N mp^2)
+    def run_op(kind, in0, in1, out):
+        op = _abi.NsOp(kind, in0, in1, out, 0, 0)
+        _abi.check(lib.mmuon_ns_run_op(C.byref(gl.struct), C.byref(op), coeffs, C.c_float(0.0), stream),
+                   "mmuon_ns_run_op")
+        torch.cuda.synchronize()
+
+    run_op(_abi.NSOP_SYMM, _abi.NSB_P, _abi.NSB_A, _abi.NSB_X1_S0)
+    run_op(_abi.NSOP_SYMM, _abi.NSB_A, _abi.NSB_P, _abi.NSB_X1_S1)
+    sub = ws.x1.view(torch.bfloat16)[: 2 * nb * mp * mp]
+    pa = panels(sub[: nb * mp * mp], nb, mp, mp)
+    ap = panels(sub[nb * mp * mp:], nb, mp, mp)
+    check_upper_tiles(pa, full_p @ full_a, "SYMM P A")
+    check_upper_tiles(ap, full_a @ full_p, "SYMM A P")
+
+
+def test_run_op_rejects_invalid_ops():
+    """mmuon_ns_run_op validates buffer kinds, overlaps and sub-stack room on the
+    host before any launch."""
+    g = torch.zeros(1, 256, 256, device=DEV)
+    (gl,) = MuonPlanner().plan([torch.zeros_like(g, dtype=torch.bfloat16)], [g.bfloat16()], [g.clone()],
+                               torch.bfloat16)
+    lib, stream = _abi.lib(), _abi.stream_handle(DEV)
+    coeffs = (C.c_float * 3)(*NS_COEFFS)
+    bad = [(_abi.NSOP_SYMM, _abi.NSB_A, _abi.NSB_P, _abi.NSB_A),          # output is an operand
+           (_abi.NSOP_SYMM, _abi.NSB_A, _abi.NSB_P, _abi.NSB_X1_S0),      # 256 x 256: no sub-stack room
+           (_abi.NSOP_PX, _abi.NSB_P, _abi.NSB_X0, _abi.NSB_X0),          # PX in place
+           (_abi.NSOP_SYRK, _abi.NSB_A, -1, _abi.NSB_P),                   # SYRK of a symmetric stack
+           (9, _abi.NSB_A, _abi.NSB_P, _abi.NSB_X1)]
+    for kind, i0, i1, o in bad:
+        op = _abi.NsOp(kind, i0, i1, o, 0, 0)
+        rc = lib.mmuon_ns_run_op(C.byref(gl.struct), C.byref(op), coeffs, C.c_float(0.0), stream)
+        assert rc == -1, (kind, i0, i1, o, rc)
