@@ -53,7 +53,7 @@ def log(*a):
 
 
 # ---------------------------------------------------------------- workload
-def build_gpu(w, device, seed=0):
+def build_gpu(w, device, seed=0, ns_form="auto"):
     from monarch_muon_amd import CoatStateMonarchMuon, MonarchMuonOptimizer, QuantizationConfig, _abi
     from monarch_muon_amd.workloads import parameter_inventory
     gen = torch.Generator(device=device).manual_seed(seed)
@@ -66,7 +66,7 @@ def build_gpu(w, device, seed=0):
             bufs.append(torch.randn(shape, generator=gen, device=device) * 1e-3)
     if w.momentum_dtype == "fp8":
         opt = CoatStateMonarchMuon(muon, adamw, lr=0.02, momentum=0.95, qargs=QuantizationConfig(),
-                                   ns_dtype=w.ns_dtype)
+                                   ns_dtype=w.ns_dtype, ns_form=ns_form)
         for p, b in zip(muon, bufs):
             st = opt.state[p]
             groups = (b.numel() + 127) // 128
@@ -77,7 +77,7 @@ def build_gpu(w, device, seed=0):
             for key, t in zip(("scale", "expand", "sqrt_minmax"), meta):
                 st[f"{key}_momentum_buffer"] = t
     else:
-        opt = MonarchMuonOptimizer(muon, adamw, lr=0.02, momentum=0.95, ns_dtype=w.ns_dtype)
+        opt = MonarchMuonOptimizer(muon, adamw, lr=0.02, momentum=0.95, ns_dtype=w.ns_dtype, ns_form=ns_form)
         for p, b in zip(muon, bufs):
             opt.state[p]["momentum_buffer"] = b.to(w.momentum_dtype)
     del bufs
@@ -986,6 +986,9 @@ def main():
     ap.add_argument("--workload", default="6.89b-nb4")
     ap.add_argument("--tokens", type=int, default=4096, help="butterfly workloads: rows of the layer input")
     ap.add_argument("--instrumented", type=int, default=2, help="extra per-kernel-timed steps")
+    ap.add_argument("--ns-form", choices=("auto", "standard"), default="auto",
+                    help="Newton-Schulz evaluation order (the optimizer's ns_form): auto = the Gram form for "
+                         "the rectangular bf16 groups, standard = the three-product chain everywhere")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--grad-clip", type=float, default=0.0,
                     help="also clip the gradient norm before every timed step (opt.clip_grad_norm_), and report "
@@ -1043,7 +1046,7 @@ def main():
     w = WORKLOADS[args.workload]
     dev = torch.device("cuda", 0)
     log(f"[bench] building workload {w.name} on {torch.cuda.get_device_name(dev)}")
-    muon, adamw, opt = build_gpu(w, dev)
+    muon, adamw, opt = build_gpu(w, dev, ns_form=args.ns_form)
     freeze_gc()
     log(f"[bench] warm-up {args.warmup} steps")
     for _ in range(args.warmup):
@@ -1112,6 +1115,7 @@ def main():
                    "momentum_dtype": w.momentum_dtype if isinstance(w.momentum_dtype, str)
                    else str(w.momentum_dtype).split(".")[-1],
                    "newton_schulz": "bf16 MFMA, fp32 accumulate, 5 iterations",
+                   "ns_form": args.ns_form,
                    "groups": [f"{gl.rows}x{gl.cols}x{gl.nblocks}" for gl in opt._muon_planner.groups]},
         "median_event_ms": round(median_ms, 3),
         "event_ms": {"min": round(min(step_ms), 3), "mean": round(statistics.mean(step_ms), 3),
