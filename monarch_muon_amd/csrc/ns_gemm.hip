@@ -6,6 +6,9 @@
 //   PX   : X' = s * P X                         (m x n, K = m)
 //   PX_APPLY (last iteration): param += alpha * bf16(X') written straight into
 //          the parameter blocks, un-transposed for tall blocks.
+//   SYMM : C = S1 S2 of two symmetric stacks that commute (the Gram form of the
+//          rectangular groups: iterations on m x m polynomials of X0 X0^T; the
+//          launch plans are built in abi.hip)
 // s = 1/(||X0||_F + 1e-7) on the first iteration (the Frobenius normalisation
 // folded into the products: (sX)(sX)^T = s^2 XX^T and P(sX) = s PX), 1
 // afterwards.  The a X term of the quintic is carried by P's diagonal: POLY adds
