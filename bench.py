@@ -734,6 +734,60 @@ def stage_table(args, w):
     print(json.dumps({"workload": w.name, "stages": rows}))
 
 
+def vendor_gemm(args, w):
+    """The vendor library's bf16 GEMM rate against the contraction length K
+    (hipBLASLt through torch.mm, M = N = 8192, K = 1024 ... 8192; and the batched
+    shape of the 1024 x 1024 group's PX), beside this build's PX launch of that
+    group, all in one process: what a GEMM with PX's K = 1024 reaches on this GPU."""
+    from monarch_muon_amd import _abi
+    from monarch_muon_amd.optim import _COEFFS
+    from monarch_muon_amd.plan import NS_STEPS
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(1)
+
+    def timed(fn, reps=20):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    rows = []
+    for k in (1024, 2048, 4096, 8192):
+        A = torch.randn(8192, k, device=dev, generator=g).bfloat16()
+        B = torch.randn(k, 8192, device=dev, generator=g).bfloat16()
+        Out = torch.empty(8192, 8192, device=dev, dtype=torch.bfloat16)
+        ms = timed(lambda: torch.mm(A, B, out=Out))
+        rows.append({"case": f"torch.mm bf16 8192 x 8192 x {k} (hipBLASLt)", "k": k, "ms": round(ms, 4),
+                     "tflops": round(2.0 * 8192 * 8192 * k / (ms * 1e-3) / 1e12, 1)})
+        log(f"[vendor] {rows[-1]}")
+        del A, B, Out
+    A = torch.randn(1408, 1024, 1024, device=dev, generator=g).bfloat16()
+    B = torch.randn(1408, 1024, 1024, device=dev, generator=g).bfloat16()
+    Out = torch.empty_like(A)
+    ms = timed(lambda: torch.bmm(A, B, out=Out))
+    rows.append({"case": "torch.bmm bf16 1408 x 1024 x 1024 x 1024 (hipBLASLt, PX's shape)", "k": 1024,
+                 "ms": round(ms, 4), "tflops": round(2.0 * 1408 * 1024 ** 3 / (ms * 1e-3) / 1e12, 1)})
+    log(f"[vendor] {rows[-1]}")
+    del A, B, Out
+    muon, adamw, opt = build_gpu(w, dev)
+    opt.step()
+    torch.cuda.synchronize()
+    lib = _abi.lib()
+    gl = opt._muon_planner.groups[0]
+    stream = _abi.stream_handle(dev)
+    ms = timed(lambda: _abi.check(lib.mmuon_ns_stage(C.byref(gl.struct), 1, NS_STEPS, 2, _COEFFS, 0.0, 0, stream),
+                                  "mmuon_ns_stage"))
+    rows.append({"case": f"ns_px_bf16<2> PX, {gl.rows}x{gl.cols}x{gl.nblocks} group (this build)", "k": gl.rows,
+                 "ms": round(ms, 4), "tflops": round(stage_exec_flops("px", gl) / (ms * 1e-3) / 1e12, 1)})
+    log(f"[vendor] {rows[-1]}")
+    print(json.dumps({"metric": "bf16 GEMM TFLOP/s against K", "rows": rows}), flush=True)
+
+
 def power_profile(args, w):
     """Each kernel of one optimizer step on the 1024 x 1024 group (and the
     AdamW group, and the whole step) launched back to back for about two
@@ -1001,6 +1055,8 @@ def main():
     ap.add_argument("--power", action="store_true",
                     help="only measure socket power, GFX clock and energy per step kernel")
     ap.add_argument("--power-seconds", type=float, default=2.0)
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="only measure hipBLASLt's bf16 GEMM rate against K beside this build's PX launch")
     ap.add_argument("--stage-table", action="store_true",
                     help="time each Newton-Schulz stage per group: ms, algorithmic GB/s, executed TFLOP/s")
     ap.add_argument("--traffic-summary", nargs=5,
@@ -1034,6 +1090,9 @@ def main():
         return
     if args.power:
         power_profile(args, WORKLOADS[args.workload])
+        return
+    if args.vendor_gemm:
+        vendor_gemm(args, WORKLOADS[args.workload])
         return
     if args.stage_table:
         stage_table(args, WORKLOADS[args.workload])

@@ -221,11 +221,13 @@ def _build(w, draws, device, opt_cls, **kw):
     return muon, adamw, opt, bufs
 
 
-@pytest.mark.parametrize("name,layers,rows", [("toy", None, None), ("257m-nb2", 2, 512), ("1.3b-nb4", 1, 256),
-                                              ("6.89b-nb4", 1, 256), ("6.89b-nb4-bf16mom", 1, 256)])
-def test_workload_step_matches_oracle(name, layers, rows):
+@pytest.mark.parametrize("name,layers,rows,form", [("toy", None, None, "auto"), ("257m-nb2", 2, 512, "auto"),
+                                                   ("1.3b-nb4", 1, 256, "auto"), ("1.3b-nb4", 1, 256, "standard"),
+                                                   ("6.89b-nb4", 1, 256, "auto"), ("6.89b-nb4", 1, 256, "standard"),
+                                                   ("6.89b-nb4-bf16mom", 1, 256, "auto")])
+def test_workload_step_matches_oracle(name, layers, rows, form):
     w, draws = _workload_params(name, layers, rows)
-    gm, ga, gopt, _ = _build(w, draws, DEV, MonarchMuonOptimizer, ns_dtype=w.ns_dtype)
+    gm, ga, gopt, _ = _build(w, draws, DEV, MonarchMuonOptimizer, ns_dtype=w.ns_dtype, ns_form=form)
     variant = "membench" if w.ns_dtype == torch.bfloat16 else "pretrain"
     cm, ca, copt, _ = _build(w, draws, "cpu", ReferenceMonarchMuon, variant=variant)
     # bf16 momentum: the update as torch's GPU kernels execute the reference's

@@ -176,3 +176,14 @@ def _gram_no_restart(x0, rnd):
         if k < 4:
             a = rnd(p @ rnd(p @ a))
     return rnd(s * (q @ x0))
+
+
+def test_optimizer_ns_form_selects_the_plan_flags():
+    """``ns_form`` maps to the plan flags; anything else is rejected at
+    construction (no GPU call)."""
+    from monarch_muon_amd import MonarchMuonOptimizer
+    p = torch.zeros(2, 8, 8, requires_grad=True)
+    assert MonarchMuonOptimizer([p], [])._ns_flags == 0
+    assert MonarchMuonOptimizer([p], [], ns_form="standard")._ns_flags == _abi.NS_STANDARD
+    with pytest.raises(ValueError):
+        MonarchMuonOptimizer([p], [], ns_form="gram")
