@@ -53,7 +53,7 @@ def log(*a):
 
 
 # ---------------------------------------------------------------- workload
-def build_gpu(w, device, seed=0, ns_form="auto"):
+def build_gpu(w, device, seed=0, ns_form="auto", merge=True):
     from monarch_muon_amd import CoatStateMonarchMuon, MonarchMuonOptimizer, QuantizationConfig, _abi
     from monarch_muon_amd.workloads import parameter_inventory
     gen = torch.Generator(device=device).manual_seed(seed)
@@ -81,6 +81,7 @@ def build_gpu(w, device, seed=0, ns_form="auto"):
         for p, b in zip(muon, bufs):
             opt.state[p]["momentum_buffer"] = b.to(w.momentum_dtype)
     del bufs
+    opt._muon_planner.merge = merge
     torch.cuda.synchronize()
     return muon, adamw, opt
 
@@ -91,29 +92,41 @@ def instrumented_step(opt, lr=0.02):
     stream the kernels run on).  Returns [(kernel, group, seconds_event_pair)]."""
     from monarch_muon_amd import _abi
     from monarch_muon_amd.optim import _COEFFS
-    from monarch_muon_amd.plan import NS_STEPS
+    from monarch_muon_amd.plan import NS_STEPS, BatchLaunch
     lib = _abi.lib()
     out = []
     muon_group, adam_group = opt.param_groups
     fp8 = type(opt).__name__ == "CoatStateMonarchMuon"
-    for gl in opt._muon_planner.groups:
-        stream = _abi.stream_handle(gl.key[0])
+
+    def timed(kind, gl, it, fn):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
+        fn()
+        e1.record()
+        out.append((kind, gl, it, e0, e1))
+
+    def pack(gl, stream):
         if fp8:
             _abi.check(lib.mmuon_fp8_momentum_pack(C.byref(gl.struct), 0.95, 1, stream), "pack")
         else:
             _abi.check(lib.mmuon_momentum_pack(C.byref(gl.struct), 0.95, stream), "pack")
-        e1.record()
-        out.append(("pack", gl, 0, e0, e1))
-        # the launches of mmuon_newton_schulz_apply, one op at a time
-        for op in _abi.ns_plan(gl.rows, gl.cols, gl.struct.ns_dtype, NS_STEPS, opt._ns_flags):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            _abi.check(lib.mmuon_ns_run_op(C.byref(gl.struct), C.byref(op), _COEFFS, -lr * gl.alpha_scale,
-                                           stream), "mmuon_ns_run_op")
-            e1.record()
-            out.append((OP_KIND[op.kind], gl, op.iteration, e0, e1))
+
+    def run_op(unit, op, alpha, stream):
+        _abi.check(lib.mmuon_ns_run_op(C.byref(unit.struct), C.byref(op), _COEFFS, alpha, stream),
+                   "mmuon_ns_run_op")
+
+    # the launches of a step, one at a time, unit by unit (plan.run_newton_schulz)
+    for u in opt._muon_planner.units:
+        members = u.members if isinstance(u, BatchLaunch) else [u]
+        stream = _abi.stream_handle(members[0].key[0])
+        for gl in members:
+            timed("pack", gl, 0, lambda: pack(gl, stream))
+        ops = _abi.ns_plan(u.rows, u.cols, u.struct.ns_dtype, NS_STEPS, opt._ns_flags)
+        for op in ops[:-1]:
+            timed(OP_KIND[op.kind], u, op.iteration, lambda: run_op(u, op, 0.0, stream))
+        for gl in members:
+            timed(OP_KIND[ops[-1].kind], gl, ops[-1].iteration,
+                  lambda: run_op(gl, ops[-1], -lr * gl.alpha_scale, stream))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     opt._adamw_step(adam_group, lr)
@@ -964,22 +977,29 @@ def traffic_summary(args):
 
     fs, ws_ = seq(fetch_csv, "FETCH_SIZE"), seq(write_csv, "WRITE_SIZE")
     from monarch_muon_amd import _abi
-    groups = [("1024x1024", 1408, 1024, 1024), ("2752x1024", 256, 2752, 1024), ("1024x2752", 128, 1024, 2752)]
-    # the instrumented step launches, per group, the pack and then the ops of its plan
-    plans = [_abi.ns_plan(r, c, _abi.BF16, 5) for _, _, r, c in groups]
-    total = sum(1 + len(ops) for ops in plans)
+    # the instrumented step's launches, unit by unit: the packs of the unit's
+    # groups, the ops of its plan but the last over all its blocks, the last op
+    # per group (the 6.89B units: the square group; the tall and wide groups)
+    units = [[("1024x1024", 1408)], [("2752x1024", 256), ("1024x2752", 128)]]
+    seq = []
+    for members in units:
+        n_all = sum(N for _, N in members)
+        name = "+".join(g for g, _ in members)
+        ops = _abi.ns_plan(1024, 1024 if members[0][0] == "1024x1024" else 2752, _abi.BF16, 5)
+        seq += [None] * len(members)
+        seq += [(name, n_all, op) for op in ops[:-1]]
+        seq += [(g, N, ops[-1]) for g, N in members]
     per_group = []
-    if len(fs) >= total and len(fs) == len(ws_):
-        last_f, last_w = fs[-total:], ws_[-total:]
-        base = 0
-        for (name, N, _, _), ops in zip(groups, plans):
-            for j, op in enumerate(ops, start=1):
-                k, fk = last_f[base + j]
-                per_group.append({"group": name, "iteration": op.iteration, "kernel": k,
-                                  "read_mib_per_block": round(fk * 1024 * fscale / N / 2 ** 20, 3),
-                                  "write_mib_per_block": round(last_w[base + j][1] * 1024 * wscale / N / 2 ** 20,
-                                                               3)})
-            base += 1 + len(ops)
+    if len(fs) >= len(seq) and len(fs) == len(ws_):
+        last_f, last_w = fs[-len(seq):], ws_[-len(seq):]
+        for j, item in enumerate(seq):
+            if item is None:
+                continue
+            name, N, op = item
+            k, fk = last_f[j]
+            per_group.append({"group": name, "iteration": op.iteration, "kernel": k,
+                              "read_mib_per_block": round(fk * 1024 * fscale / N / 2 ** 20, 3),
+                              "write_mib_per_block": round(last_w[j][1] * 1024 * wscale / N / 2 ** 20, 3)})
     Path(out_path).write_text(json.dumps({"calibration": {"fetch_scale": fscale, "write_scale": wscale},
                                           "kernels": kernels, "per_group": per_group}, indent=1) + "\n")
     print(json.dumps({k: round(v["bytes"] / 1e9, 3) for k, v in kernels.items()}, indent=1))
@@ -1040,6 +1060,9 @@ def main():
     ap.add_argument("--workload", default="6.89b-nb4")
     ap.add_argument("--tokens", type=int, default=4096, help="butterfly workloads: rows of the layer input")
     ap.add_argument("--instrumented", type=int, default=2, help="extra per-kernel-timed steps")
+    ap.add_argument("--separate-groups", action="store_true",
+                    help="launch every group's Newton-Schulz on its own (by default a tall group and its wide "
+                         "counterpart share their launches)")
     ap.add_argument("--ns-form", choices=("auto", "standard"), default="auto",
                     help="Newton-Schulz evaluation order (the optimizer's ns_form): auto = the Gram form for "
                          "the rectangular bf16 groups, standard = the three-product chain everywhere")
@@ -1105,7 +1128,7 @@ def main():
     w = WORKLOADS[args.workload]
     dev = torch.device("cuda", 0)
     log(f"[bench] building workload {w.name} on {torch.cuda.get_device_name(dev)}")
-    muon, adamw, opt = build_gpu(w, dev, ns_form=args.ns_form)
+    muon, adamw, opt = build_gpu(w, dev, ns_form=args.ns_form, merge=not args.separate_groups)
     freeze_gc()
     log(f"[bench] warm-up {args.warmup} steps")
     for _ in range(args.warmup):
@@ -1174,7 +1197,7 @@ def main():
                    "momentum_dtype": w.momentum_dtype if isinstance(w.momentum_dtype, str)
                    else str(w.momentum_dtype).split(".")[-1],
                    "newton_schulz": "bf16 MFMA, fp32 accumulate, 5 iterations",
-                   "ns_form": args.ns_form,
+                   "ns_form": args.ns_form, "shared_launches": not args.separate_groups,
                    "groups": [f"{gl.rows}x{gl.cols}x{gl.nblocks}" for gl in opt._muon_planner.groups]},
         "median_event_ms": round(median_ms, 3),
         "event_ms": {"min": round(min(step_ms), 3), "mean": round(statistics.mean(step_ms), 3),

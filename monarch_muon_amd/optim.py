@@ -26,7 +26,8 @@ import ctypes as C
 import torch
 
 from . import _abi
-from .plan import NORM_CHUNK, NS_COEFFS, NS_STEPS, AdamPlanner, MuonPlanner, NormPlanner, adamw_scalars
+from .plan import (NORM_CHUNK, NS_COEFFS, NS_STEPS, AdamPlanner, MuonPlanner, NormPlanner, adamw_scalars,
+                   run_newton_schulz)
 
 _COEFFS = (C.c_float * 3)(*NS_COEFFS)
 
@@ -68,7 +69,6 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
         self._adam_planner = AdamPlanner()
         self._norm_planner = NormPlanner()
         self._clip = None    # device clipping coefficient for the next step (clip_grad_norm_)
-        self._timing = None  # optional per-launch hipEvent capture, used by bench.py
 
     # ------------------------------------------------------------------
     @torch.no_grad()
@@ -166,20 +166,17 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
         if not params:
             return
         bufs = [self._get_momentum_buffer(p) for p in params]
-        launches = self._muon_planner.plan(params, grads, bufs, self.ns_dtype)
+        self._muon_planner.plan(params, grads, bufs, self.ns_dtype)
         momentum = float(group["momentum"])
         lib = _abi.lib()
-        for gl in launches:
-            stream = _abi.stream_handle(gl.key[0])
-            gl.struct.grad_scale = self._grad_scale()
-            ev = self._mark("pack")
+        gscale = self._grad_scale()
+
+        def pack(gl, stream):
+            gl.struct.grad_scale = gscale
             _abi.check(lib.mmuon_momentum_pack(C.byref(gl.struct), momentum, stream), "mmuon_momentum_pack")
-            self._mark_end(ev)
-            ev = self._mark("ns", gl)
-            _abi.check(lib.mmuon_newton_schulz_apply(C.byref(gl.struct), NS_STEPS, _COEFFS,
-                                                     -lr * gl.alpha_scale, self._ns_flags, stream),
-                       "mmuon_newton_schulz_apply")
-            self._mark_end(ev)
+
+        run_newton_schulz(self._muon_planner.units, lib, _COEFFS, lr, self._ns_flags, NS_STEPS,
+                          lambda gl: _abi.stream_handle(gl.key[0]), pack)
 
     # ------------------------------------------------------------------
     # AdamW (membench :176-208; pretrain :171-201 keeps a step per tensor)
@@ -232,13 +229,11 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
                               grad_dtype=_abi.dtype_code(al.gd), state_dtype=_abi.dtype_code(al.sd),
                               grad_scale=self._grad_scale(), **adamw_scalars(lr, beta1, beta2, eps, wd, step))
         stream = _abi.stream_handle(al.tensors.device)
-        ev = self._mark("adamw")
         if al.fp8 is not None:
             _abi.check(lib.mmuon_adamw_fp8(C.byref(args), C.cast(al.fp8.data_ptr(), C.POINTER(_abi.AdamWFp8Tensor)),
                                            int(have_state), stream), "mmuon_adamw_fp8")
         else:
             _abi.check(lib.mmuon_adamw(C.byref(args), stream), "mmuon_adamw")
-        self._mark_end(ev)
 
     def _adamw_split(self, al, params, grads, ms, vs, kinds, lr, beta1, beta2, eps, wd, fp8_meta):
         lib = _abi.lib()
@@ -254,18 +249,6 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
     # ------------------------------------------------------------------
     # optional per-launch timing (bench.py): hipEvents on the launch stream
     # ------------------------------------------------------------------
-    def _mark(self, name, gl=None):
-        if self._timing is None:
-            return None
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        return (name, gl, s, e)
-
-    def _mark_end(self, ev):
-        if ev is None:
-            return
-        ev[3].record()
-        self._timing.append(ev)
 
 
 # ---------------------------------------------------------------------------
@@ -352,21 +335,18 @@ class CoatStateMonarchMuon(MonarchMuonOptimizer):
         key_dtypes = [torch.float32 if "momentum_buffer" in self.state[p] else p.dtype for p in params]
         bufs = [self._ensure_fp8(self.state[p], "momentum_buffer", p) for p in params]
         meta = [self._meta(self.state[p], "momentum_buffer") for p in params]
-        launches = self._muon_planner.plan(params, grads, bufs, self.ns_dtype, fp8_meta=meta, key_dtypes=key_dtypes)
+        self._muon_planner.plan(params, grads, bufs, self.ns_dtype, fp8_meta=meta, key_dtypes=key_dtypes)
         momentum = float(group["momentum"])
         lib = _abi.lib()
-        for gl in launches:
-            stream = _abi.stream_handle(gl.key[0])
-            gl.struct.grad_scale = self._grad_scale()
-            ev = self._mark("pack")
+        gscale = self._grad_scale()
+
+        def pack(gl, stream):
+            gl.struct.grad_scale = gscale
             _abi.check(lib.mmuon_fp8_momentum_pack(C.byref(gl.struct), momentum, 1, stream),
                        "mmuon_fp8_momentum_pack")
-            self._mark_end(ev)
-            ev = self._mark("ns", gl)
-            _abi.check(lib.mmuon_newton_schulz_apply(C.byref(gl.struct), NS_STEPS, _COEFFS,
-                                                     -lr * gl.alpha_scale, self._ns_flags, stream),
-                       "mmuon_newton_schulz_apply")
-            self._mark_end(ev)
+
+        run_newton_schulz(self._muon_planner.units, lib, _COEFFS, lr, self._ns_flags, NS_STEPS,
+                          lambda gl: _abi.stream_handle(gl.key[0]), pack)
 
     def _adamw_step(self, group: dict, lr: float) -> None:
         params = [p for p in group["params"] if p.grad is not None]

@@ -81,13 +81,27 @@ class Workspace:
     scale: torch.Tensor
 
     @classmethod
-    def allocate(cls, rows, cols, ns_code, nblocks, device) -> "Workspace":
+    def allocate(cls, rows, cols, ns_code, nblocks, device, nparts: int = 0) -> "Workspace":
+        """Stacks for ``nblocks`` blocks; ``nparts``: partial sums per block to
+        make room for (at least the geometry's own)."""
         lay = _abi.ns_layout(rows, cols, ns_code, nblocks)
         u8 = dict(dtype=torch.uint8, device=device)
+        part = nblocks * max(nparts, lay.nparts) * 4
         return cls(lay, torch.zeros(lay.x_bytes, **u8), torch.zeros(lay.x_bytes, **u8),
                    torch.empty(lay.a_bytes, **u8), torch.empty(lay.a_bytes, **u8),
-                   torch.empty(max(lay.part_bytes, 4), **u8),
+                   torch.empty(max(part, 4), **u8),
                    torch.empty(nblocks, dtype=torch.float32, device=device))
+
+    def view(self, lay: _abi.NsLayout, b0: int, nblocks: int, pstride: int) -> "Workspace":
+        """Blocks ``b0 .. b0 + nblocks`` of these stacks as a workspace of their
+        own with layout ``lay`` (same m, n, mp, np, dtype); ``pstride``: the
+        partial sums reserved per block in this allocation."""
+        xb = self.x0.numel() // self.scale.numel()   # bytes per block of each stack
+        ab = self.a.numel() // self.scale.numel()
+        pb = 4 * pstride
+        return Workspace(lay, self.x0[b0 * xb:(b0 + nblocks) * xb], self.x1[b0 * xb:(b0 + nblocks) * xb],
+                         self.a[b0 * ab:(b0 + nblocks) * ab], self.p[b0 * ab:(b0 + nblocks) * ab],
+                         self.partial[b0 * pb:(b0 + nblocks) * pb], self.scale[b0:b0 + nblocks])
 
     def x_view(self, which: int, dtype: torch.dtype, nblocks: int) -> torch.Tensor:
         """The X stack (``which`` = 0 or 1) as ``[N, mp, np]``.  fp32 stacks are
@@ -117,6 +131,8 @@ class GroupLaunch:
     kofs: np.ndarray | None = None        # block index within its parameter, per row
     grad_block_bytes: int = 0
     grad_dtype: torch.dtype | None = None
+    ns_code: int = 0
+    batch: "BatchLaunch | None" = None   # set when the group shares its Newton-Schulz launches
 
     @property
     def alpha_scale(self) -> float:
@@ -125,6 +141,48 @@ class GroupLaunch:
     @property
     def transposed(self) -> bool:
         return self.rows > self.cols
+
+
+@dataclass
+class BatchLaunch:
+    """Groups of one Newton-Schulz geometry (device, NS dtype, m = min(r, c),
+    n = max(r, c)) -- a tall group and its wide counterpart, e.g. 2752 x 1024
+    and 1024 x 2752.  After the pack their blocks are all m x n stacks of the
+    same layout, held in consecutive views of one workspace, so every
+    Newton-Schulz launch but the last runs once over all of them; the last one
+    (the apply) runs per group, with its parameters, orientation and
+    ``sqrt(rows/cols)``.  Block results do not depend on the batch they run in,
+    so this changes launches, not values."""
+    members: list                 # GroupLaunch, in plan order
+    ws: Workspace
+    nblocks: int
+    struct: _abi.Group = field(default_factory=_abi.Group)
+
+    @property
+    def rows(self) -> int:
+        return self.struct.rows
+
+    @property
+    def cols(self) -> int:
+        return self.struct.cols
+
+    @property
+    def transposed(self) -> bool:
+        return False
+
+    def refresh(self) -> None:
+        """Struct fields that follow the members' tables (rebuilt with new
+        gradients).  The batch's launches never read the block table (only the
+        apply does, and it runs per member); it points at the first member's."""
+        s, first = self.struct, self.members[0].struct
+        s.blocks = first.blocks
+        s.flags = 0
+        s.grad_scale = None
+
+
+def ns_geometry(gl: "GroupLaunch"):
+    """The key groups share Newton-Schulz launches under: (device, NS dtype, m, n)."""
+    return (gl.key[0], gl.ns_code, min(gl.rows, gl.cols), max(gl.rows, gl.cols))
 
 
 class MuonPlanner:
@@ -136,20 +194,32 @@ class MuonPlanner:
     tensors each step while everything else stays; then only the gradient
     column of each group's block table is recomputed and uploaded."""
 
-    def __init__(self):
+    def __init__(self, merge: bool = True):
         self._sig = None
         self._gptr = None
         self._groups: list[GroupLaunch] = []
+        self._units: list = []
         self._ws: dict = {}
+        # groups of one Newton-Schulz geometry share their launches (BatchLaunch)
+        self.merge = merge
 
     @property
     def groups(self) -> list[GroupLaunch]:
+        """The reference's groups, in its order."""
         return self._groups
+
+    @property
+    def units(self) -> list:
+        """Execution units in group order: a GroupLaunch, or a BatchLaunch for
+        groups that share their Newton-Schulz launches (placed at its first
+        member)."""
+        return self._units
 
     def release(self) -> None:
         self._sig = None
         self._gptr = None
         self._groups = []
+        self._units = []
         self._ws = {}
 
     def plan(self, params, grads, bufs, ns_dtype: torch.dtype, fp8_meta=None, key_dtypes=None) -> list[GroupLaunch]:
@@ -172,6 +242,7 @@ class MuonPlanner:
         keys = bufs if key_dtypes is None else [_KeyView(b, d) for b, d in zip(bufs, key_dtypes)]
         self._groups = [self._build(key, idx, params, grads, bufs, ns_dtype, fp8_meta)
                         for key, idx in plan_groups(keys).items()]
+        self._link()
         self._sig, self._gptr = sig, gptr
         return self._groups
 
@@ -195,19 +266,54 @@ class MuonPlanner:
             gl.table = _h2d_int64(rows_tab, gl.key[0])
             gl.struct.blocks = gl.table.data_ptr()
             gl.struct.flags = _abi.GROUP_ALIGNED16 if not bool(np.any(rows_tab % 16)) else 0
+        for u in self._units:
+            if isinstance(u, BatchLaunch):
+                u.refresh()
         self._gptr = gptr
         return True
 
-    def _workspace(self, rows, cols, ns_code, nblocks, device) -> Workspace:
-        """One workspace per (geometry, NS dtype, device), grown to the largest
-        group seen.  Groups of one step run one after another on one stream, so
-        two groups of the same geometry share it safely."""
-        k = (rows, cols, ns_code, device)
+    def _workspace(self, m, n, ns_code, nblocks, device, pstride) -> Workspace:
+        """One workspace per Newton-Schulz geometry (m <= n, NS dtype, device),
+        grown to the largest batch seen; ``pstride`` partial sums per block."""
+        k = (m, n, ns_code, device)
         ws = self._ws.get(k)
-        if ws is None or ws.scale.numel() < nblocks:
+        if ws is None or ws.scale.numel() < nblocks or ws.partial.numel() < nblocks * pstride * 4:
             self._ws[k] = None  # drop the smaller one before allocating
-            ws = self._ws[k] = Workspace.allocate(rows, cols, ns_code, nblocks, device)
+            ws = self._ws[k] = Workspace.allocate(m, n, ns_code, nblocks, device, pstride)
         return ws
+
+    def _link(self) -> None:
+        """Give every group its workspace (consecutive views of one allocation
+        per Newton-Schulz geometry) and form the execution units."""
+        by_geo: "OrderedDict[tuple, list[GroupLaunch]]" = OrderedDict()
+        for gl in self._groups:
+            by_geo.setdefault(ns_geometry(gl) if self.merge else (id(gl),), []).append(gl)
+        self._units = []
+        for gls in by_geo.values():
+            device, ns_code, m, n = ns_geometry(gls[0])
+            lays = [_abi.ns_layout(gl.rows, gl.cols, ns_code, gl.nblocks) for gl in gls]
+            pstride = max(lay.nparts for lay in lays)
+            total = sum(gl.nblocks for gl in gls)
+            ws = self._workspace(m, n, ns_code, total, device, pstride)
+            b0 = 0
+            for gl, lay in zip(gls, lays):
+                gl.ws = ws.view(lay, b0, gl.nblocks, pstride)
+                _point_at(gl.struct, gl.ws)
+                gl.batch = None
+                b0 += gl.nblocks
+            if len(gls) == 1:
+                self._units.append(gls[0])
+                continue
+            b = BatchLaunch(gls, ws.view(_abi.ns_layout(m, n, ns_code, total), 0, total, pstride), total)
+            s, f = b.struct, gls[0].struct
+            s.rows, s.cols, s.nblocks = m, n, total
+            s.param_dtype, s.grad_dtype, s.buf_dtype, s.ns_dtype = f.param_dtype, f.grad_dtype, f.buf_dtype, ns_code
+            s.fp8 = None
+            _point_at(s, b.ws)
+            b.refresh()
+            for gl in gls:
+                gl.batch = b
+            self._units.append(b)
 
     def _build(self, key, idx, params, grads, bufs, ns_dtype, fp8_meta) -> GroupLaunch:
         device, kdtype, rows, cols = key
@@ -230,7 +336,6 @@ class MuonPlanner:
             ns_code = _abi.dtype_code(kdtype)
         counts = np.array([bufs[i].shape[0] for i in idx], dtype=np.int64)
         nblocks = int(counts.sum())
-        ws = self._workspace(rows, cols, ns_code, nblocks, device)
         es = np.array([params[idx[0]].element_size(), grads[idx[0]].element_size(),
                        bufs[idx[0]].element_size()], dtype=np.int64) * rc
         bases = np.array([(params[i].data_ptr(), grads[i].data_ptr(), bufs[i].data_ptr()) for i in idx],
@@ -243,8 +348,8 @@ class MuonPlanner:
         if fp8_meta is not None:
             mb = np.array([tuple(t.data_ptr() for t in fp8_meta[i]) for i in idx], dtype=np.int64)
             fp8_table = _h2d_int64(np.repeat(mb, counts, axis=0) + k[:, None] * (rc // 128 * 4), device)
-        gl = GroupLaunch(key, rows, cols, nblocks, list(idx), ws, table, fp8_table, rows_tab=rows_tab,
-                         counts=counts, kofs=k, grad_block_bytes=int(es[1]), grad_dtype=gd)
+        gl = GroupLaunch(key, rows, cols, nblocks, list(idx), None, table, fp8_table, rows_tab=rows_tab,
+                         counts=counts, kofs=k, grad_block_bytes=int(es[1]), grad_dtype=gd, ns_code=ns_code)
         s = gl.struct
         s.rows, s.cols, s.nblocks = rows, cols, nblocks
         s.param_dtype, s.grad_dtype = _abi.dtype_code(pd), _abi.dtype_code(gd)
@@ -253,10 +358,37 @@ class MuonPlanner:
         s.flags = _abi.GROUP_ALIGNED16 if aligned else 0
         s.blocks = table.data_ptr()
         s.fp8 = fp8_table.data_ptr() if fp8_table is not None else None
-        s.x0, s.x1 = ws.x0.data_ptr(), ws.x1.data_ptr()
-        s.a, s.p = ws.a.data_ptr(), ws.p.data_ptr()
-        s.partial, s.scale = ws.partial.data_ptr(), ws.scale.data_ptr()
-        return gl
+        return gl   # workspace pointers: _link
+
+
+def _point_at(s: _abi.Group, ws: Workspace) -> None:
+    s.x0, s.x1 = ws.x0.data_ptr(), ws.x1.data_ptr()
+    s.a, s.p = ws.a.data_ptr(), ws.p.data_ptr()
+    s.partial, s.scale = ws.partial.data_ptr(), ws.scale.data_ptr()
+
+
+def run_newton_schulz(units, lib, coeffs, lr: float, flags: int, iters: int, stream_of, pack) -> None:
+    """One step's Muon launches, unit by unit: the pack of every group (``pack(gl,
+    stream)``), then Newton-Schulz and the apply -- ``mmuon_newton_schulz_apply``
+    for a lone group; for a batch, its plan's ops but the last over all member
+    blocks, then the last op (the apply) per member with its own alpha."""
+    for u in units:
+        if isinstance(u, BatchLaunch):
+            stream = stream_of(u.members[0])
+            for gl in u.members:
+                pack(gl, stream)
+            ops = _abi.ns_plan(u.rows, u.cols, u.struct.ns_dtype, iters, flags)
+            for op in ops[:-1]:
+                _abi.check(lib.mmuon_ns_run_op(C.byref(u.struct), C.byref(op), coeffs, 0.0, stream),
+                           "mmuon_ns_run_op")
+            for gl in u.members:
+                _abi.check(lib.mmuon_ns_run_op(C.byref(gl.struct), C.byref(ops[-1]), coeffs,
+                                               -lr * gl.alpha_scale, stream), "mmuon_ns_run_op")
+        else:
+            stream = stream_of(u)
+            pack(u, stream)
+            _abi.check(lib.mmuon_newton_schulz_apply(C.byref(u.struct), iters, coeffs, -lr * u.alpha_scale,
+                                                     flags, stream), "mmuon_newton_schulz_apply")
 
 
 # ---------------------------------------------------------------------------

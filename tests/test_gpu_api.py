@@ -182,3 +182,56 @@ def test_fresh_gradient_tensors_each_step_equal_fixed_ones(case_idx, fp8):
     torch.cuda.synchronize()
     for p, q in zip(m1 + a1, m2 + a2):
         assert torch.equal(p, q)
+
+
+def _layer(name, seed=3):
+    """One layer's Monarch factors of a workload (bf16 params and grads) and a
+    short AdamW tensor, drawn on the GPU."""
+    from monarch_muon_amd.workloads import WORKLOADS, parameter_inventory
+    w = WORKLOADS[name]
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    muon, adamw = [], []
+    for n, s, is_muon in parameter_inventory(w):
+        if is_muon and (".h." not in n or int(n.split(".")[2]) > 0):
+            continue
+        if not is_muon:
+            s = (64,) + tuple(s[1:]) if len(s) == 2 else s
+        p = (torch.randn(s, generator=gen, device=DEV) * 0.02).bfloat16()
+        p.grad = (torch.randn(s, generator=gen, device=DEV) * 1e-3).bfloat16()
+        (muon if is_muon else adamw).append(p)
+    return muon, adamw[:2]
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["fp32mom", "fp8"])
+@pytest.mark.parametrize("name", ["1.3b-nb4", "6.89b-nb4"])
+def test_shared_newton_schulz_launches_equal_per_group_launches(name, fp8):
+    """Groups of one Newton-Schulz geometry (a tall group and its wide
+    counterpart, e.g. 2752 x 1024 and 1024 x 2752) share every launch but the
+    apply; two steps that way give the bits of two steps with each group
+    launched on its own (the reference's one batch per shape)."""
+    from monarch_muon_amd.plan import BatchLaunch
+    m1, a1 = _layer(name)
+    m2, a2 = _layer(name)
+    mk = (lambda m, a: CoatStateMonarchMuon(m, a, lr=0.02, momentum=0.95, qargs=QuantizationConfig())) if fp8 \
+        else (lambda m, a: MonarchMuonOptimizer(m, a, lr=0.02, momentum=0.95))
+    o1, o2 = mk(m1, a1), mk(m2, a2)
+    o2._muon_planner.merge = False
+    if not fp8:
+        gen = torch.Generator(device=DEV).manual_seed(9)
+        for p, q in zip(m1, m2):
+            b = torch.randn(p.shape, generator=gen, device=DEV) * 1e-3
+            o1.state[p]["momentum_buffer"], o2.state[q]["momentum_buffer"] = b, b.clone()
+    for _ in range(2):
+        o1.step()
+        o2.step()
+    torch.cuda.synchronize()
+    batches = [u for u in o1._muon_planner.units if isinstance(u, BatchLaunch)]
+    assert [[(g.rows, g.cols) for g in b.members] for b in batches] == \
+        ([[(1376, 512), (512, 1376)]] if name == "1.3b-nb4" else [[(2752, 1024), (1024, 2752)]])
+    assert not any(isinstance(u, BatchLaunch) for u in o2._muon_planner.units)
+    for p, q in zip(m1 + a1, m2 + a2):
+        assert torch.equal(p, q)
+        s1, s2 = o1.state[p], o2.state[q]
+        for k in s1:
+            if torch.is_tensor(s1[k]):
+                assert torch.equal(_bits(s1[k]), _bits(s2[k])), k
