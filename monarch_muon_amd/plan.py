@@ -157,6 +157,14 @@ class BatchLaunch:
     ws: Workspace
     nblocks: int
     struct: _abi.Group = field(default_factory=_abi.Group)
+    _plans: dict = field(default_factory=dict)
+
+    def plan(self, iters: int, flags: int) -> list:
+        """The ops ``mmuon_newton_schulz_apply`` would launch for these blocks."""
+        k = (iters, flags)
+        if k not in self._plans:
+            self._plans[k] = _abi.ns_plan(self.rows, self.cols, self.struct.ns_dtype, iters, flags)
+        return self._plans[k]
 
     @property
     def rows(self) -> int:
@@ -377,7 +385,7 @@ def run_newton_schulz(units, lib, coeffs, lr: float, flags: int, iters: int, str
             stream = stream_of(u.members[0])
             for gl in u.members:
                 pack(gl, stream)
-            ops = _abi.ns_plan(u.rows, u.cols, u.struct.ns_dtype, iters, flags)
+            ops = u.plan(iters, flags)
             for op in ops[:-1]:
                 _abi.check(lib.mmuon_ns_run_op(C.byref(u.struct), C.byref(op), coeffs, 0.0, stream),
                            "mmuon_ns_run_op")
