@@ -208,8 +208,19 @@ class MuonPlanner:
         self._groups: list[GroupLaunch] = []
         self._units: list = []
         self._ws: dict = {}
-        # groups of one Newton-Schulz geometry share their launches (BatchLaunch)
-        self.merge = merge
+        self._merge = merge
+
+    @property
+    def merge(self) -> bool:
+        """Whether groups of one Newton-Schulz geometry share their launches
+        (BatchLaunch); changing it rebuilds the plan at the next step."""
+        return self._merge
+
+    @merge.setter
+    def merge(self, on: bool) -> None:
+        if bool(on) != self._merge:
+            self._merge = bool(on)
+            self._sig = None
 
     @property
     def groups(self) -> list[GroupLaunch]:
