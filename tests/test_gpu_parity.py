@@ -38,7 +38,7 @@ def blocks_rel(a, b):
 
 # ---------------------------------------------------------------- Newton-Schulz alone
 NS_SHAPES = [(4, 256, 256), (2, 512, 1368), (2, 1376, 512), (2, 1024, 1024), (1, 1024, 2752),
-             (2, 96, 136), (2, 136, 96), (3, 64, 64)]
+             (2, 96, 136), (2, 136, 96), (3, 64, 64), (2, 96, 600), (1, 600, 96)]
 
 
 def run_ns_only(g: torch.Tensor, ns_dtype, flags: int = 0) -> torch.Tensor:

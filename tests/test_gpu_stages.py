@@ -33,7 +33,7 @@ from monarch_muon_amd.plan import NS_COEFFS, MuonPlanner
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
 TILE = 256
-SHAPES = [(2, 1024, 1024), (1, 2752, 1024), (1, 1024, 2752), (3, 512, 512), (2, 96, 136),
+SHAPES = [(2, 1024, 1024), (1, 2752, 1024), (1, 1024, 2752), (3, 512, 512), (2, 96, 136), (2, 96, 600),
           (40, 1024, 1024), (30, 1024, 2752)]
 
 
@@ -132,6 +132,9 @@ def test_stage_outputs_against_fp64_products(shape):
     ap = panels(sub[nb * mp * mp:], nb, mp, mp)
     check_upper_tiles(pa, full_p @ full_a, "SYMM P A")
     check_upper_tiles(ap, full_a @ full_p, "SYMM A P")
+    # zero padding of both operands gives zero padding, the diagonal included
+    if lay.m < mp:
+        assert float(pa[:, lay.m:, :].abs().max()) == 0.0 and float(ap[:, :, lay.m:].abs().max()) == 0.0
 
 
 def test_run_op_rejects_invalid_ops():
