@@ -848,6 +848,21 @@ def power_profile(args, w):
     flops = {cases[1][0]: stage_exec_flops("syrk", gl), cases[2][0]: stage_exec_flops("poly", gl),
              cases[3][0]: stage_exec_flops("px", gl), cases[4][0]: stage_exec_flops("px", gl),
              cases[7][0]: 2.0 * bm * 1024 ** 3, cases[8][0]: 2.0 * 8192 ** 3}
+    # the Gram-form stages of the shared rectangular unit (2752 x 1024 + 1024 x 2752 blocks)
+    from monarch_muon_amd.plan import BatchLaunch
+    for u in opt._muon_planner.units:
+        if not isinstance(u, BatchLaunch):
+            continue
+        name = "+".join(f"{m.rows}x{m.cols}" for m in u.members)
+        ops = {o.kind: o for o in u.plan(NS_STEPS, opt._ns_flags)}
+        sy = _abi.NsOp(_abi.NSOP_SYMM, _abi.NSB_P, _abi.NSB_A, _abi.NSB_X1_S0, 0, 0)
+        for kind, op in (("syrk", ops.get(_abi.NSOP_SYRK)), ("poly", ops.get(_abi.NSOP_POLY)), ("symm", sy)):
+            if op is None:
+                continue
+            label = f"{kernel_symbol(kind, u, 1)} {kind.upper()} ({name} unit, {u.nblocks} blocks)"
+            cases.append((label, (lambda u=u, op=op: _abi.check(
+                lib.mmuon_ns_run_op(C.byref(u.struct), C.byref(op), _COEFFS, 0.0, stream), "mmuon_ns_run_op"))))
+            flops[label] = stage_exec_flops(kind, u)
     rows = []
     time.sleep(1.0)
     sampler.start()
