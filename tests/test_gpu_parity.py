@@ -128,9 +128,18 @@ def test_ns_fp32_against_fp64_truth(shape):
     assert rel_fro(ours, truth).max() < 2e-5
 
 
-def test_ns_zero_block_gives_zero():
-    g = torch.zeros(2, 256, 256, device=DEV)
+@pytest.mark.parametrize("shape", [(2, 256, 256), (2, 256, 688), (2, 688, 256)], ids=lambda s: "x".join(map(str, s)))
+def test_ns_zero_block_gives_zero(shape):
+    """A zero block stays zero, alone and beside a non-zero block of the same
+    stack (the Gram form's polynomials of a zero Gram matrix are a^k I, finite,
+    applied to a zero X)."""
+    g = torch.zeros(shape, device=DEV)
     assert torch.count_nonzero(run_ns_only(g, torch.bfloat16)) == 0
+    g[1] = torch.randn(shape[1:], generator=torch.Generator().manual_seed(3)).to(DEV) * 1e-3
+    out = run_ns_only(g, torch.bfloat16)
+    assert torch.count_nonzero(out[0]) == 0 and bool(torch.isfinite(out).all())
+    truth = ns_fp64(g[1:].cpu().to(torch.bfloat16).double())
+    assert float(rel_fro(out[1:], truth).max()) < 0.03
 
 
 # ---------------------------------------------------------------- golden vectors (reference-written)
