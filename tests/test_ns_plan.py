@@ -187,3 +187,19 @@ def test_optimizer_ns_form_selects_the_plan_flags():
     assert MonarchMuonOptimizer([p], [], ns_form="standard")._ns_flags == _abi.NS_STANDARD
     with pytest.raises(ValueError):
         MonarchMuonOptimizer([p], [], ns_form="gram")
+
+
+def test_plan_entry_point_validates_its_arguments():
+    """mmuon_ns_plan: the op count with a NULL array, MMUON_ERANGE when the
+    array is too short, MMUON_EINVAL for a bad iteration count, shape or dtype
+    (host-only calls)."""
+    import ctypes as C
+    lib = _abi.lib()
+    n = lib.mmuon_ns_plan(1024, 2752, _abi.BF16, 5, 0, None, 0)
+    assert n == 18
+    short = (_abi.NsOp * 4)()
+    assert lib.mmuon_ns_plan(1024, 2752, _abi.BF16, 5, 0, short, 4) == -3
+    for args in [(1024, 2752, _abi.BF16, 0), (1024, 2752, _abi.BF16, 65), (0, 2752, _abi.BF16, 5),
+                 (1024, 2752, 7, 5)]:
+        assert lib.mmuon_ns_plan(*args, 0, None, 0) == -1, args
+    assert lib.mmuon_ns_plan(1024, 1024, _abi.F32, 5, 0, None, 0) == 15
