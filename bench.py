@@ -801,6 +801,84 @@ def vendor_gemm(args, w):
     print(json.dumps({"metric": "bf16 GEMM TFLOP/s against K", "rows": rows}), flush=True)
 
 
+def power_rows(sampler, cases, flops, seconds, nbytes=None):
+    """Each case launched back to back for about ``seconds``: ms per launch,
+    sampled socket power and GFX clock, the limiters' share of the interval;
+    executed TFLOP/s for the cases in ``flops``, GB/s for those in ``nbytes``.
+    The first row is the idle GPU."""
+    nbytes = nbytes or {}
+    rows = []
+    time.sleep(1.0)
+    sampler.start()
+    time.sleep(1.0)
+    idle = sampler.stop(skip_s=0.2)
+    rows.append({"kernel": "idle (nothing launched)", **idle})
+    for name, fn in cases:
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        one = time.perf_counter() - t0
+        n = max(3, int(seconds / max(one, 1e-4)))
+        sampler.start()
+        time.sleep(0.05)
+        v0 = sampler.violations()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        v1 = sampler.violations()
+        st = sampler.stop()
+        ms = a.elapsed_time(b) / n
+        row = {"kernel": name, "launches": n, "ms": round(ms, 4), **st}
+        ticks = v1.get("acc_counter", 0) - v0.get("acc_counter", 0)
+        if ticks > 0:
+            row["limited_frac"] = {k[4:]: round((v1[k] - v0[k]) / ticks, 3) for k in v0
+                                   if k != "acc_counter" and k in v1}
+        if name in flops:
+            row["exec_tflops"] = round(flops[name] / (ms * 1e-3) / 1e12, 1)
+        if name in nbytes:
+            row["gbs"] = round(nbytes[name] / (ms * 1e-3) / 1e9, 1)
+        rows.append(row)
+        log(f"[bench] {name}: {ms:.3f} ms, {st['socket_w']} W, {st['gfx_mhz']} MHz")
+        time.sleep(0.5)
+    return rows
+
+
+def data_energy(args):
+    """HBM power against the data moved: the same streams (read, and copy
+    between two regions, 4 GiB each, 1024-thread workgroups streaming
+    contiguous spans) over all-zero and over random-looking data, and the write
+    probe's hashed data, each launched back to back under the power sampler."""
+    from monarch_muon_amd import _abi
+    lib = _abi.lib()
+    dev = torch.device("cuda", 0)
+    nbytes = 4 << 30
+    gen = torch.Generator(device=dev).manual_seed(0)
+    rnd = torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), dtype=torch.int32, device=dev, generator=gen)
+    zero = torch.zeros_like(rnd)
+    dst = torch.empty_like(rnd)
+    stream = _abi.stream_handle(dev)
+    sampler = PowerSampler(dev)
+
+    def probe(kind, src, nt, out=None):
+        return lambda: _abi.check(lib.mmuon_hbm_stream(kind, out, src.data_ptr(), nbytes, nt, 16384, stream),
+                                  "mmuon_hbm_stream")
+
+    cases = [("read, all-zero data", probe(3, zero, 1)), ("read, random data", probe(3, rnd, 1)),
+             ("copy, all-zero data", probe(5, zero, 1, dst.data_ptr())),
+             ("copy, random data", probe(5, rnd, 1, dst.data_ptr())),
+             ("write, hashed data", probe(4, rnd, 0, dst.data_ptr()))]
+    moved = {"read, all-zero data": nbytes, "read, random data": nbytes, "copy, all-zero data": 2 * nbytes,
+             "copy, random data": 2 * nbytes, "write, hashed data": nbytes}
+    rows = power_rows(sampler, cases, {}, args.power_seconds, moved)
+    print(json.dumps({"metric": "socket power / GFX clock against the data streamed", "bytes": nbytes,
+                      "power_cap_w": sampler.power_cap_w(), "rows": rows}), flush=True)
+
+
 def power_profile(args, w):
     """Each kernel of one optimizer step on the 1024 x 1024 group (and the
     AdamW group, and the whole step) launched back to back for about two
@@ -863,45 +941,7 @@ def power_profile(args, w):
             cases.append((label, (lambda u=u, op=op: _abi.check(
                 lib.mmuon_ns_run_op(C.byref(u.struct), C.byref(op), _COEFFS, 0.0, stream), "mmuon_ns_run_op"))))
             flops[label] = stage_exec_flops(kind, u)
-    rows = []
-    time.sleep(1.0)
-    sampler.start()
-    time.sleep(1.0)
-    idle = sampler.stop(skip_s=0.2)
-    rows.append({"kernel": "idle (nothing launched)", **idle})
-    for name, fn in cases:
-        fn()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        fn()
-        torch.cuda.synchronize()
-        one = time.perf_counter() - t0
-        n = max(3, int(args.power_seconds / max(one, 1e-4)))
-        sampler.start()
-        time.sleep(0.05)
-        v0 = sampler.violations()
-        e0, t0 = sampler.energy_j(), time.perf_counter()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(n):
-            fn()
-        b.record()
-        torch.cuda.synchronize()
-        t1, e1 = time.perf_counter(), sampler.energy_j()
-        v1 = sampler.violations()
-        st = sampler.stop()
-        ms = a.elapsed_time(b) / n
-        row = {"kernel": name, "launches": n, "ms": round(ms, 4), **st,
-               "energy_j_per_launch": round((e1 - e0) / n, 3), "energy_w": round((e1 - e0) / (t1 - t0), 1)}
-        ticks = v1.get("acc_counter", 0) - v0.get("acc_counter", 0)
-        if ticks > 0:
-            row["limited_frac"] = {k[4:]: round((v1[k] - v0[k]) / ticks, 3) for k in v0
-                                   if k != "acc_counter" and k in v1}
-        if name in flops:
-            row["exec_tflops"] = round(flops[name] / (ms * 1e-3) / 1e12, 1)
-        rows.append(row)
-        log(f"[bench] {name}: {ms:.3f} ms, {st['socket_w']} W, {st['gfx_mhz']} MHz")
-        time.sleep(0.5)
+    rows = power_rows(sampler, cases, flops, args.power_seconds)
     print(json.dumps({"metric": "socket power / GFX clock / energy per kernel", "workload": w.name,
                       "group": f"{gl.rows}x{gl.cols}x{gl.nblocks}", "power_cap_w": sampler.power_cap_w(),
                       "rows": rows}), flush=True)
@@ -1093,6 +1133,8 @@ def main():
     ap.add_argument("--power", action="store_true",
                     help="only measure socket power, GFX clock and energy per step kernel")
     ap.add_argument("--power-seconds", type=float, default=2.0)
+    ap.add_argument("--data-energy", action="store_true",
+                    help="only measure socket power and clock while streaming all-zero against random data")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="only measure hipBLASLt's bf16 GEMM rate against K beside this build's PX launch")
     ap.add_argument("--stage-table", action="store_true",
@@ -1131,6 +1173,9 @@ def main():
         return
     if args.vendor_gemm:
         vendor_gemm(args, WORKLOADS[args.workload])
+        return
+    if args.data_energy:
+        data_energy(args)
         return
     if args.stage_table:
         stage_table(args, WORKLOADS[args.workload])
