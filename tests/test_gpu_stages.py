@@ -154,3 +154,30 @@ def test_run_op_rejects_invalid_ops():
         op = _abi.NsOp(kind, i0, i1, o, 0, 0)
         rc = lib.mmuon_ns_run_op(C.byref(gl.struct), C.byref(op), coeffs, C.c_float(0.0), stream)
         assert rc == -1, (kind, i0, i1, o, rc)
+
+
+@pytest.mark.parametrize("shape", [(3, 1024, 2752), (2, 512, 512)], ids=lambda s: "x".join(map(str, s)))
+def test_plan_ops_one_by_one_equal_newton_schulz_apply(shape):
+    """The ops of ``mmuon_ns_plan`` run one at a time through
+    ``mmuon_ns_run_op`` (how bench.py times each launch) give the bits of
+    ``mmuon_newton_schulz_apply`` (Gram form and three-product chain)."""
+    gen = torch.Generator().manual_seed(5)
+    g = (torch.randn(shape, generator=gen) * 1e-3).to(DEV)
+    outs = []
+    for one_by_one in (False, True):
+        p = torch.zeros_like(g, dtype=torch.bfloat16)
+        (gl,) = MuonPlanner().plan([p], [g.bfloat16()], [torch.zeros_like(g)], torch.bfloat16)
+        lib, stream = _abi.lib(), _abi.stream_handle(DEV)
+        coeffs = (C.c_float * 3)(*NS_COEFFS)
+        _abi.check(lib.mmuon_momentum_pack(C.byref(gl.struct), 0.0, stream), "pack")
+        ops = _abi.ns_plan(gl.rows, gl.cols, _abi.BF16, 5, _abi.NS_NO_APPLY)
+        if one_by_one:
+            for op in ops:
+                _abi.check(lib.mmuon_ns_run_op(C.byref(gl.struct), C.byref(op), coeffs, C.c_float(0.0), stream),
+                           "mmuon_ns_run_op")
+        else:
+            _abi.check(lib.mmuon_newton_schulz_apply(C.byref(gl.struct), 5, coeffs, 0.0, _abi.NS_NO_APPLY, stream),
+                       "mmuon_newton_schulz_apply")
+        torch.cuda.synchronize()
+        outs.append(gl.ws.x_view(ops[-1].out, torch.bfloat16, gl.nblocks).clone())
+    assert torch.equal(outs[0], outs[1])
