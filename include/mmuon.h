@@ -132,12 +132,16 @@ int mmuon_fp8_momentum_pack(const mmuon_group* g, float momentum, int32_t have_s
    Gram form (see mmuon_ns_plan).  flags: MMUON_NS_NO_APPLY leaves the final X
    in the workspace stack named by the plan's last op (standard chain: x0 when
    iters is even, x1 otherwise; Gram form: x0) and does not touch params;
-   MMUON_NS_STANDARD selects the three-product chain for every group.
+   MMUON_NS_STANDARD selects the three-product chain for every group;
+   MMUON_NS_HOLD_LAST launches every op of the plan but the last (for groups
+   sharing their launches: the last op, the apply, then runs per group through
+   mmuon_ns_run_op).
    Replaces membench monarch_muon.py:36-50 (_newton_schulz_batched, with the
    norm at :38-39), :164-170 (cast back, split, _foreach_add_ apply);
    pretrain monarch_muon.py:36-50,159-165. */
 #define MMUON_NS_NO_APPLY 1
 #define MMUON_NS_STANDARD 2
+#define MMUON_NS_HOLD_LAST 4
 int mmuon_newton_schulz_apply(const mmuon_group* g, int32_t iters, const float coeffs[3],
                               float alpha, int32_t flags, void* stream);
 

@@ -17,6 +17,7 @@ F32, BF16, F8E4M3 = 0, 1, 2
 GROUP_ALIGNED16 = 1
 NS_NO_APPLY = 1
 NS_STANDARD = 2
+NS_HOLD_LAST = 4
 ABI_VERSION = 6
 # Newton-Schulz plan ops (MMUON_NSOP_*) and buffers (MMUON_NSB_*)
 NSOP_SYRK, NSOP_POLY, NSOP_PX, NSOP_PX_APPLY, NSOP_SYMM = 0, 1, 2, 3, 4

@@ -405,8 +405,9 @@ int mmuon_newton_schulz_apply(const mmuon_group* g, int32_t iters, const float c
   const hipStream_t s = static_cast<hipStream_t>(stream);
   std::vector<mmuon_ns_op> plan;
   build_plan(geo, g->ns_dtype, iters, flags, plan);
-  for (const mmuon_ns_op& op : plan)
-    if (int rc = run_op(g, geo, op, coeffs, alpha, s)) return rc;
+  const size_t nrun = (flags & MMUON_NS_HOLD_LAST) ? plan.size() - 1 : plan.size();
+  for (size_t i = 0; i < nrun; ++i)
+    if (int rc = run_op(g, geo, plan[i], coeffs, alpha, s)) return rc;
   return check_launch("mmuon_newton_schulz_apply");
 }
 

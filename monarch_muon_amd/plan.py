@@ -389,17 +389,17 @@ def _point_at(s: _abi.Group, ws: Workspace) -> None:
 def run_newton_schulz(units, lib, coeffs, lr: float, flags: int, iters: int, stream_of, pack) -> None:
     """One step's Muon launches, unit by unit: the pack of every group (``pack(gl,
     stream)``), then Newton-Schulz and the apply -- ``mmuon_newton_schulz_apply``
-    for a lone group; for a batch, its plan's ops but the last over all member
-    blocks, then the last op (the apply) per member with its own alpha."""
+    for a lone group; for a batch, the same call with ``NS_HOLD_LAST`` over all
+    member blocks (every op of the plan but the last), then the last op (the
+    apply) per member with its own alpha."""
     for u in units:
         if isinstance(u, BatchLaunch):
             stream = stream_of(u.members[0])
             for gl in u.members:
                 pack(gl, stream)
             ops = u.plan(iters, flags)
-            for op in ops[:-1]:
-                _abi.check(lib.mmuon_ns_run_op(C.byref(u.struct), C.byref(op), coeffs, 0.0, stream),
-                           "mmuon_ns_run_op")
+            _abi.check(lib.mmuon_newton_schulz_apply(C.byref(u.struct), iters, coeffs, 0.0,
+                                                     flags | _abi.NS_HOLD_LAST, stream), "mmuon_newton_schulz_apply")
             for gl in u.members:
                 _abi.check(lib.mmuon_ns_run_op(C.byref(gl.struct), C.byref(ops[-1]), coeffs,
                                                -lr * gl.alpha_scale, stream), "mmuon_ns_run_op")
