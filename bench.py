@@ -880,10 +880,11 @@ def data_energy(args):
 
 
 def power_profile(args, w):
-    """Each kernel of one optimizer step on the 1024 x 1024 group (and the
-    AdamW group, and the whole step) launched back to back for about two
-    seconds: ms per launch, socket power, GFX clock, and energy per launch
-    from the energy counter."""
+    """Each kernel of one optimizer step on the 1024 x 1024 group, the
+    Gram-form stages of the shared rectangular unit, the AdamW group, the whole
+    step and two vendor-library products, each launched back to back for about
+    two seconds: ms per launch, socket power, GFX clock and the share of the
+    interval the power limiter held the clock (power_rows)."""
     from monarch_muon_amd import _abi
     from monarch_muon_amd.optim import _COEFFS
     from monarch_muon_amd.plan import NS_STEPS
@@ -1131,7 +1132,7 @@ def main():
                     help="steps of the fresh-gradient leg (host planner time); 0 skips it")
     ap.add_argument("--hbm-ceiling", action="store_true", help="only measure read / write / copy bandwidth")
     ap.add_argument("--power", action="store_true",
-                    help="only measure socket power, GFX clock and energy per step kernel")
+                    help="only measure socket power, GFX clock and the power limiter per step kernel")
     ap.add_argument("--power-seconds", type=float, default=2.0)
     ap.add_argument("--data-energy", action="store_true",
                     help="only measure socket power and clock while streaming all-zero against random data")
