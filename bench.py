@@ -593,8 +593,8 @@ def hbm_ceiling(args):
 
 # ---------------------------------------------------------------- power and clock
 class PowerSampler:
-    """Socket power, GFX clock and the energy counter of this GPU (amdsmi),
-    sampled from a thread every few ms."""
+    """Socket power and GFX clock of this GPU (amdsmi), sampled from a thread
+    every few ms, and the firmware's throttle accumulators."""
 
     def __init__(self, device):
         import amdsmi
@@ -611,10 +611,6 @@ class PowerSampler:
                     self.h = h
         self.samples = []
         self._stop = None
-
-    def energy_j(self):
-        e = self.smi.amdsmi_get_energy_count(self.h)
-        return e["energy_accumulator"] * e["counter_resolution"] * 1e-6
 
     VIOLATIONS = ("acc_counter", "acc_ppt_pwr", "acc_socket_thrm", "acc_vr_thrm", "acc_hbm_thrm", "acc_prochot_thrm")
 
