@@ -44,6 +44,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "optimizer-step ms, 6.89B-ref nb=4 bf16; NS TFLOP/s as % of bf16 MFMA peak"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_F32_TFLOPS = 157.3     # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0
 REFERENCE_H100_MS = 304.4   # README.md:16 (bf16 momentum, H100)
 
@@ -182,6 +183,10 @@ def stage_exec_flops(kind, gl):
     32x32 MFMA tiles on or above the diagonal)."""
     lay = gl.ws.layout
     N, mp, np_ = gl.nblocks, lay.mp, lay.np_
+    if gl.struct.ns_dtype == 0:   # fp32 kernels: every tile of the padded products
+        kx = -(-lay.n // 32) * 32   # SYRK's K: n rounded up to the 32-deep K tiles
+        full = {"syrk": mp * mp * kx, "poly": mp ** 3, "px": mp * mp * np_, "px_apply": mp * mp * np_}
+        return 2.0 * full.get(kind, 0) * N
     nt = mp // 256
     sym = (nt * (nt - 1) / 2 + nt * 36 / 64) / (nt * nt)
     kx = -(-lay.n // 32) * 32   # SYRK's K: n rounded up to the 32-deep slices
@@ -676,6 +681,10 @@ def stage_bytes(kind, gl):
     parameter block read and written instead of X'."""
     lay = gl.ws.layout
     N, mp, np_ = gl.nblocks, lay.mp, lay.np_
+    if gl.struct.ns_dtype == 0:   # fp32 kernels: every tile of the padded products
+        kx = -(-lay.n // 32) * 32   # SYRK's K: n rounded up to the 32-deep K tiles
+        full = {"syrk": mp * mp * kx, "poly": mp ** 3, "px": mp * mp * np_, "px_apply": mp * mp * np_}
+        return 2.0 * full.get(kind, 0) * N
     nt = mp // 256
     up = nt * (nt + 1) // 2 * 256 * 256 * 2
     kx = -(-lay.n // 32) * 32
@@ -1240,11 +1249,16 @@ def main():
                for k, v in sorted(per.items(), key=lambda kv: -kv[1][0])}
     mom_bytes = 4 if w.momentum_dtype == torch.float32 else (2 if w.momentum_dtype == torch.bfloat16 else 1)
     pack_ms = stage_ms["pack"] / reps
-    pack_b = sum(pack_bytes(gl, mom_bytes) for gl in opt._muon_planner.groups)
+    gbytes = torch.empty((), dtype=w.param_dtype).element_size()
+    pack_b = sum(pack_bytes(gl, mom_bytes, gbytes, 4 if gl.struct.ns_dtype == 0 else 2)
+                 for gl in opt._muon_planner.groups)
+    # Newton-Schulz in fp32 (the pretrain copy with fp32 momentum): priced against the fp32 MFMA peak
+    ns32 = w.ns_dtype is None and w.momentum_dtype in (torch.float32, "fp8")
+    peak = PEAK_F32_TFLOPS if ns32 else PEAK_BF16_TFLOPS
     res = {
         "metric": METRIC, "value": round(wall_ms, 3), "unit": "ms", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(wall_ms, 3), "higher_is_better": False,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32" if ns32 else "bf16",
         "data": "synthetic (seeded N(0,.02) weights, N(0,1e-3) grads and momentum, resident in HBM)",
         "config": {"workload": w.name, "layers": w.n_layer, "hidden": w.n_embd, "intermediate": w.intermediate,
                    **({"shard": f"rank 0 of {w.shards}: the Muon blocks of layers 0-{local_layers(w) - 1} and 1/{w.shards} "
@@ -1253,7 +1267,7 @@ def main():
                    "param_dtype": str(w.param_dtype).split(".")[-1],
                    "momentum_dtype": w.momentum_dtype if isinstance(w.momentum_dtype, str)
                    else str(w.momentum_dtype).split(".")[-1],
-                   "newton_schulz": "bf16 MFMA, fp32 accumulate, 5 iterations",
+                   "newton_schulz": ("fp32 MFMA" if ns32 else "bf16 MFMA, fp32 accumulate") + ", 5 iterations",
                    "ns_form": args.ns_form, "shared_launches": not args.separate_groups,
                    "groups": [f"{gl.rows}x{gl.cols}x{gl.nblocks}" for gl in opt._muon_planner.groups]},
         "median_event_ms": round(median_ms, 3),
@@ -1265,25 +1279,28 @@ def main():
                                           "(benchmark_train_step.py:297-299,386-397: 3 warm-ups, median of 12 "
                                           "event-timed steps; this script's defaults)"},
         "roofline": {"bound": "mfma", "kernel": dominant, "achieved": round(achieved, 1),
-                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                      "traffic": traffic, "avg_launch_ms": round(d_avg, 4),
                      "alg_flops_per_launch": d_fl / d_n, "exec_tflops": round((d_ex / d_n) / (d_avg * 1e-3) / 1e12, 1),
-                     **({"exec_frac": round((d_ex / d_n) / (d_avg * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                     **({"exec_frac": round((d_ex / d_n) / (d_avg * 1e-3) / 1e12 / peak, 4),
                          "counters": {"source": f"profiles/mfma_util_{w.name}.json",
                                       **{k: counters[k] for k in ("exec_frac_peak", "exec_frac_at_clock",
                                                                   "mfma_busy", "gfx_mhz") if k in counters}}}
                         if counters else {})},
         "newton_schulz": {"ms": round(ns_ms, 3), "alg_tflop": round(ns_flops(w) / 1e12, 2),
-                          "alg_tflops": round(ns_tf, 1), "frac_peak": round(ns_tf / PEAK_BF16_TFLOPS, 4),
+                          "alg_tflops": round(ns_tf, 1), "chain_equiv_frac_peak": round(ns_tf / peak, 4),
                           "exec_tflop": round(ns_exec / 1e12, 2),
                           "exec_tflops": round(ns_exec / (ns_ms * 1e-3) / 1e12, 1),
-                          "exec_frac_peak": round(ns_exec / (ns_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                          "exec_frac_peak": round(ns_exec / (ns_ms * 1e-3) / 1e12 / peak, 4),
+                          "peak_tflops": peak,
                           "forms": {f"{gl.rows}x{gl.cols}x{gl.nblocks}":
                                     "gram" if any(op.kind == 4 for op in _ns_plan(gl, opt)) else "chain"
                                     for gl in opt._muon_planner.groups},
                           "note": "alg_tflop: the reference's three-product chain (2m^2(2n+m) per block and "
                                   "iteration, symmetric products counted in full), the work every evaluation "
-                                  "order replaces; exec_tflop: the MFMA work the launched kernels execute"},
+                                  "order replaces; exec_tflop: the MFMA work the launched kernels execute; "
+                                  "chain_equiv_frac_peak: the chain's work per second over the peak, not MFMA "
+                                  "utilisation (exec_frac_peak is)"},
         "momentum_pack": {"ms": round(pack_ms, 3), "alg_bytes": pack_b,
                           "gbs": round(pack_b / (pack_ms * 1e-3) / 1e9, 1),
                           "frac_hbm": round(pack_b / (pack_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},

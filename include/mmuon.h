@@ -320,7 +320,10 @@ int mmuon_grad_clip_coef(const mmuon_grad_norm_args* a, void* stream);
    for (nchunks rounded up to 64) + ntensors; larger inputs return
    MMUON_ERANGE.  The stream must belong to the current device.  Calls on one
    stream are ordered; calls that overlap on one GPU (several streams or
-   threads) share the array and race. */
+   threads) share the array and race.  The first call on each device looks up
+   the array's device address (hipGetSymbolAddress): make that call outside
+   graph capture; later calls can be captured and replayed (the captured
+   launches hold the table, output and gradient addresses of that call). */
 #define MMUON_NOALLOC_SCRATCH_FLOATS (1 << 20)
 int mmuon_grad_clip_coef_noalloc(const mmuon_grad_norm_args* a, void* stream);
 

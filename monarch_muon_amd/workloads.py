@@ -43,6 +43,10 @@ WORKLOADS = {
     # momentum (membench/scripts/monarch_benchmark/benchmark_train_step.py:428-436 asserts bf16 states)
     "6.89b-nb4-bf16mom": Workload("6.89b-nb4-bf16mom", 32, 4096, 32, 11008, 4, torch.bfloat16, torch.bfloat16,
                                   torch.bfloat16, True),
+    # the pretrain copy at 1.3B shapes: fp32 params, grads and momentum, Newton-Schulz in the momentum dtype
+    # (pretrain/src/models/monarch/monarch_muon.py:133-165; the reference allows TF32 for these products,
+    # pretrain/src/main.py:51)
+    "1.3b-nb4-f32": Workload("1.3b-nb4-f32", 24, 2048, 16, 5504, 4, torch.float32, torch.float32, None, True),
     # one rank's share of the headline step sharded over 8 GPUs by block ownership: the Muon blocks of 4 of the
     # 32 layers (every layer has the same blocks, so whole layers balance the Newton-Schulz work) and 1/8 of the
     # AdamW group's elements (AdamW is elementwise; a rank owns a contiguous range of the flattened group)

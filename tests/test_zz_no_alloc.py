@@ -72,3 +72,35 @@ def test_noalloc_rejects_inputs_beyond_the_scratch_array():
     assert "scratch" in lib.mmuon_last_error().decode()
     torch.cuda.synchronize()
     assert float(total) == 0.0 and float(coef) == 0.0
+
+
+def test_noalloc_clip_coef_under_graph_capture():
+    """Captured into a HIP graph (after one call outside capture, which looks up
+    the scratch array's device address) and replayed on new gradient values:
+    every replay equals the workspace entry point run eagerly on the same
+    values, with the program's own eager work and synchronisations between the
+    replays."""
+    lib = _abi.lib()
+    grads = _grads(BIG[:6], torch.bfloat16, seed=50)
+    nl = NormPlanner().plan(grads)
+    t_na, c_na = torch.zeros(1, device=DEV), torch.zeros(1, device=DEV)
+    t_ws, c_ws = torch.zeros(1, device=DEV), torch.zeros(1, device=DEV)
+    b = _args(nl, t_na, c_na, 0.5, workspace=False)
+    a = _args(nl, t_ws, c_ws, 0.5, workspace=True)
+    _abi.check(lib.mmuon_grad_clip_coef_noalloc(C.byref(b), _abi.stream_handle(DEV)), "warm-up")
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _abi.check(lib.mmuon_grad_clip_coef_noalloc(C.byref(b), _abi.stream_handle(DEV)), "captured call")
+    gen = torch.Generator(device=DEV).manual_seed(51)
+    for replay in range(4):
+        for g in grads:   # new values in the same tensors (the graph holds their addresses)
+            g.copy_((torch.randn(g.shape, device=DEV, generator=gen) * 10.0 ** -(replay + 1)).to(g.dtype))
+        t_na.fill_(-1.0)
+        c_na.fill_(-1.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        _abi.check(lib.mmuon_grad_clip_coef(C.byref(a), _abi.stream_handle(DEV)), "eager workspace call")
+        torch.cuda.synchronize()
+        assert torch.equal(t_na, t_ws) and torch.equal(c_na, c_ws), (replay, t_na, t_ws, c_na, c_ws)
+    del graph
