@@ -108,7 +108,8 @@ def instrumented_step(opt, lr=0.02):
 
     def pack(gl, stream):
         if fp8:
-            _abi.check(lib.mmuon_fp8_momentum_pack(C.byref(gl.struct), 0.95, 1, stream), "pack")
+            _abi.check(lib.mmuon_fp8_momentum_pack(C.byref(gl.struct), 0.95, 1, float(opt.expand_min), stream),
+                       "pack")
         else:
             _abi.check(lib.mmuon_momentum_pack(C.byref(gl.struct), 0.95, stream), "pack")
 
@@ -543,8 +544,26 @@ def fresh_grad_leg(opt, params, steps=5):
 
 
 # ---------------------------------------------------------------- HBM ceiling
+def probe_lib():
+    """``bench_probe.so`` (built from ``bench_probe.hip`` by ``__graft_entry__.build()``):
+    the HBM streaming probe, a library of its own apart from the optimizer's."""
+    path = ROOT / "bench_probe.so"
+    if not path.exists():
+        raise RuntimeError(f"{path} is missing: build it with `python __graft_entry__.py`")
+    lib = C.CDLL(str(path))
+    lib.probe_hbm_stream.restype = C.c_int
+    lib.probe_hbm_stream.argtypes = [C.c_int32, C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_int32, C.c_void_p]
+    lib.probe_last_error.restype = C.c_char_p
+    return lib
+
+
+def probe_check(lib, rc):
+    if rc != 0:
+        raise RuntimeError(f"probe_hbm_stream failed (code {rc}): {lib.probe_last_error().decode(errors='replace')}")
+
+
 def hbm_ceiling(args):
-    """Bandwidth of 16-B vector streams over 4 GiB buffers (mmuon_hbm_stream),
+    """Bandwidth of 16-B vector streams over 4 GiB buffers (probe_hbm_stream),
     swept over launch sizes and plain / non-temporal accesses, beside torch's
     device copy.  Two launch patterns: grid-stride 256-thread workgroups (4
     accesses in flight), and 1024-thread workgroups that each stream one
@@ -552,7 +571,7 @@ def hbm_ceiling(args):
     (read and rewrite) and the momentum pack's three streams (gradient read,
     momentum read and rewritten, X written).  Bytes moved = read + written."""
     from monarch_muon_amd import _abi
-    lib = _abi.lib()
+    lib = probe_lib()
     dev = torch.device("cuda", 0)
     nbytes = 4 << 30
     gen = torch.Generator(device=dev).manual_seed(0)
@@ -583,8 +602,8 @@ def hbm_ceiling(args):
         for nt in (0, 1):
             for grid in grids:
                 d = None if kind in (0, 3) else dst.data_ptr()
-                ms = timed(lambda: _abi.check(lib.mmuon_hbm_stream(kind, d, src.data_ptr(), nbytes, nt, grid, stream),
-                                              "mmuon_hbm_stream"))
+                ms = timed(lambda: probe_check(lib, lib.probe_hbm_stream(kind, d, src.data_ptr(), nbytes, nt, grid,
+                                                                         stream)))
                 rows.append({"kind": name, "pattern": pattern, "nontemporal": nt, "grid": grid, "ms": round(ms, 4),
                              "gbs": round(moved * nbytes / (ms * 1e-3) / 1e9, 1)})
     ms = timed(lambda: dst.copy_(src))
@@ -859,7 +878,7 @@ def data_energy(args):
     contiguous spans) over all-zero and over random-looking data, and the write
     probe's hashed data, each launched back to back under the power sampler."""
     from monarch_muon_amd import _abi
-    lib = _abi.lib()
+    lib = probe_lib()
     dev = torch.device("cuda", 0)
     nbytes = 4 << 30
     gen = torch.Generator(device=dev).manual_seed(0)
@@ -870,8 +889,7 @@ def data_energy(args):
     sampler = PowerSampler(dev)
 
     def probe(kind, src, nt, out=None):
-        return lambda: _abi.check(lib.mmuon_hbm_stream(kind, out, src.data_ptr(), nbytes, nt, 16384, stream),
-                                  "mmuon_hbm_stream")
+        return lambda: probe_check(lib, lib.probe_hbm_stream(kind, out, src.data_ptr(), nbytes, nt, 16384, stream))
 
     cases = [("read, all-zero data", probe(3, zero, 1)), ("read, random data", probe(3, rnd, 1)),
              ("copy, all-zero data", probe(5, zero, 1, dst.data_ptr())),

@@ -1,14 +1,32 @@
-// HBM streaming probes: the read, write, copy, in-place update and
-// momentum-pack-pattern bandwidth this GPU sustains for 16-B vector accesses,
-// the ceilings the momentum pack and AdamW (both HBM-bound streaming kernels)
-// are measured against.  Not part of the optimizer step.
+// HBM streaming probes for bench.py (--hbm-ceiling, --data-energy): the read,
+// write, copy, in-place update and momentum-pack-pattern bandwidth this GPU
+// sustains for 16-B vector accesses, the ceilings the momentum pack and AdamW
+// (both HBM-bound streaming kernels) are measured against.  Built as its own
+// library (bench_probe.so), apart from libmmuon.so: it is not part of the
+// optimizer step or of its C ABI.
 #include <stdio.h>
 
-#include "common.hpp"
-#include "kernels.hpp"
+#include <string>
+
+#include "monarch_muon_amd/csrc/common.hpp"
 
 namespace mmuon {
 namespace {
+
+thread_local std::string g_probe_err;
+
+int set_error(int code, const char* msg) {
+  g_probe_err = msg;
+  return code;
+}
+
+int launch_status(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return MMUON_OK;
+  char msg[256];
+  snprintf(msg, sizeof msg, "%s: %s", what, hipGetErrorString(e));
+  return set_error(MMUON_EHIP, msg);
+}
 
 constexpr int SP_NT = 256;
 constexpr int SP_UNROLL = 4;
@@ -179,7 +197,23 @@ void launch_span(uint4* dst, uint4* src, int64_t n16, bool nt, int grid, hipStre
 }  // namespace
 }  // namespace mmuon
 
-extern "C" int mmuon_hbm_stream(int32_t kind, void* dst, void* src, int64_t bytes, int32_t nontemporal,
+// Streams `bytes`-long buffers with 16-B vector accesses; nontemporal != 0 uses
+// non-temporal loads and stores.
+//   kind 0 / 1 / 2: read src / write dst (hashed random-looking data) / copy
+//     src -> dst; grid x 256 threads, grid-stride, 4 accesses in flight;
+//   kind 3 / 4 / 5 / 6: read / write / copy / update dst in place; grid x 1024
+//     threads, workgroup w streams the w-th of grid contiguous spans, 8
+//     accesses in flight;
+//   kind 7: the momentum pack's three streams over spans: per 16-B gradient
+//     unit read from src's first half, two 16-B momentum units of dst read and
+//     rewritten and one 16-B unit written to src's second half (3 x bytes
+//     moved), two gradient units in flight per thread.
+// bytes a positive multiple of 32, buffers 16-B aligned; the read probes may
+// pass dst = NULL (else dst holds grid * 4096 (kind 0) or grid * 16384 (kind 3)
+// bytes).  Returns 0 or a negative MMUON_E* code (message: probe_last_error).
+extern "C" const char* probe_last_error(void) { return mmuon::g_probe_err.c_str(); }
+
+extern "C" int probe_hbm_stream(int32_t kind, void* dst, void* src, int64_t bytes, int32_t nontemporal,
                                 int32_t grid, void* stream) {
   using namespace mmuon;
   char msg[160];
@@ -214,5 +248,5 @@ extern "C" int mmuon_hbm_stream(int32_t kind, void* dst, void* src, int64_t byte
     case 6: launch_span<6>(d, sw, n16, nt, grid, s); break;
     default: launch_span<7>(d, sw, n16, nt, grid, s); break;
   }
-  return launch_status("mmuon_hbm_stream");
+  return launch_status("probe_hbm_stream");
 }

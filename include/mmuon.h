@@ -32,7 +32,8 @@ extern "C" {
 enum {
   MMUON_F32 = 0,
   MMUON_BF16 = 1,
-  MMUON_F8E4M3 = 2 /* OCP float8_e4m3fn payload, with per-128 fp32 metadata */
+  MMUON_F8E4M3 = 2, /* OCP float8_e4m3fn payload, with per-128 fp32 metadata */
+  MMUON_F8E5M2 = 3  /* OCP float8_e5m2 payload, with per-128 fp32 metadata   */
 };
 
 /* error codes */
@@ -48,7 +49,7 @@ typedef struct mmuon_block_ref {
   void* param;       /* r*c elements, row-major, param dtype      */
   const void* grad;  /* r*c elements, grad dtype                  */
   void* buf;         /* r*c elements, momentum dtype (F32/BF16), or the
-                        e4m3 payload for the FP8-state path            */
+                        FP8 payload (e4m3 / e5m2) of the FP8-state path */
 } mmuon_block_ref;
 
 /* FP8 metadata of one block: per 128-element group of the block's slice of the
@@ -80,7 +81,7 @@ typedef struct mmuon_group {
   int32_t nblocks;               /* N                                            */
   int32_t param_dtype;           /* F32 / BF16                                   */
   int32_t grad_dtype;            /* F32 / BF16                                   */
-  int32_t buf_dtype;             /* F32 / BF16 / F8E4M3                          */
+  int32_t buf_dtype;             /* F32 / BF16 / F8E4M3 / F8E5M2                 */
   int32_t ns_dtype;              /* BF16 (membench copy) or F32 (pretrain copy)  */
   int32_t flags;                 /* MMUON_GROUP_* bits                           */
   const mmuon_block_ref* blocks; /* device table, N entries                      */
@@ -112,14 +113,18 @@ int mmuon_ns_layout(int32_t rows, int32_t cols, int32_t ns_dtype, int64_t nblock
    (the transpose); pretrain monarch_muon.py:143-148,158. */
 int mmuon_momentum_pack(const mmuon_group* g, float momentum, void* stream);
 
-/* FP8-state variant of mmuon_momentum_pack: buf holds e4m3 codes with the
-   per-128 metadata of g->fp8; dequantize -> momentum -> stack/cast -> requantize.
-   `have_state` = 0 treats the momentum as zeros (first step, where the reference
-   creates it with zeros_like).  Requires rows*cols % 128 == 0.
+/* FP8-state variant of mmuon_momentum_pack: buf holds FP8 codes (buf_dtype
+   MMUON_F8E4M3 or MMUON_F8E5M2) with the per-128 metadata of g->fp8;
+   dequantize -> momentum -> stack/cast -> requantize with the codec's
+   expand_min (> 0; COAT's default 16).  `have_state` = 0 treats the momentum
+   as zeros (first step, where the reference creates it with zeros_like).
+   Requires rows*cols % 128 == 0 (every 128-group of the flattened parameter
+   inside one block; other shapes go through mmuon_fp8_dequantize, the plain
+   pack and mmuon_fp8_quantize over the whole parameter).
    Replaces coat_state_muon.py:126-139 (dequantize/quantize_ around the step,
    :94-114) fused with the work of mmuon_momentum_pack. */
 int mmuon_fp8_momentum_pack(const mmuon_group* g, float momentum, int32_t have_state,
-                            void* stream);
+                            float expand_min, void* stream);
 
 /* Newton-Schulz over the group's stack (already packed into g->x0) followed by
    the weight update:
@@ -248,8 +253,11 @@ typedef struct mmuon_adamw_args {
    :171-201.  state_dtype F32 or BF16. */
 int mmuon_adamw(const mmuon_adamw_args* a, void* stream);
 
-/* FP8-state AdamW: exp_avg (signed) and exp_avg_sq (unsigned) held as e4m3 with
-   per-128 metadata; chunk_elems must be 128 (one metadata group per chunk).
+/* FP8-state AdamW: exp_avg (signed, format a->state_dtype) and exp_avg_sq
+   (unsigned, format v_dtype), each MMUON_F8E4M3 or MMUON_F8E5M2 (the
+   reference's first_order_bit / second_order_bit), held with per-128 metadata
+   of the flattened tensor (a tensor's last group may be short); chunk_elems
+   must be 128 (one metadata group per chunk); expand_min > 0.
    have_state = 1: the moments are dequantized to fp32 and updated in fp32.
    have_state = 0: the moments are created in this step: they start from zero
    in the PARAMETER dtype and every moment op rounds to it (the wrapped step
@@ -261,17 +269,21 @@ typedef struct mmuon_adamw_fp8_tensor {
   float* scale_v; float* expand_v; float* sqrt_minmax_v;
 } mmuon_adamw_fp8_tensor;
 int mmuon_adamw_fp8(const mmuon_adamw_args* a, const mmuon_adamw_fp8_tensor* meta,
-                    int32_t have_state, void* stream);
+                    int32_t have_state, int32_t v_dtype, float expand_min, void* stream);
 
-/* Stand-alone codec over one flat tensor (numel elements):
-   quantize: fp32 values -> e4m3 codes + scale/expand/sqrt_minmax per 128-group
+/* Stand-alone codec over one flat tensor (numel elements; the last 128-group
+   may be short):
+   quantize: fp32 values -> FP8 codes (fp8_dtype MMUON_F8E4M3 or MMUON_F8E5M2)
+             + scale/expand/sqrt_minmax per 128-group, with expand_min > 0
    dequantize: the inverse.  Replaces coat_state_muon.py:94-114 (_quantize_kernel
-   :46-91, _dequantize_kernel :22-43).  signed_ = 1 for first-order states. */
+   :46-91, _dequantize_kernel :22-43; formats :17).  signed_ = 1 for
+   first-order states. */
 int mmuon_fp8_quantize(const float* value, uint8_t* codes, float* scale, float* expand,
-                       float* sqrt_minmax, int64_t numel, int32_t signed_, void* stream);
+                       float* sqrt_minmax, int64_t numel, int32_t signed_, int32_t fp8_dtype,
+                       float expand_min, void* stream);
 int mmuon_fp8_dequantize(const uint8_t* codes, const float* scale, const float* expand,
                          const float* sqrt_minmax, float* out, int64_t numel,
-                         int32_t signed_, void* stream);
+                         int32_t signed_, int32_t fp8_dtype, void* stream);
 
 /* Gradient-norm clipping folded into the step.  Computes, over the listed
    gradients (one dtype, F32 or BF16), what torch.nn.utils.clip_grad_norm_
@@ -370,25 +382,6 @@ int mmuon_butterfly_fwd(const mmuon_butterfly_args* a, void* stream);
 int mmuon_butterfly_bwd(const mmuon_butterfly_args* a, void* stream);
 /* Workspace bytes the backward needs for these shapes (x, pointers unused). */
 size_t mmuon_butterfly_workspace(const mmuon_butterfly_args* a);
-
-/* HBM streaming probe with 16-B vector accesses over `bytes`-long buffers;
-   nontemporal != 0 uses non-temporal loads and stores.
-     kind 0 / 1 / 2: read src / write dst (hashed random-looking data) / copy
-       src -> dst; grid x 256 threads, grid-stride, 4 accesses in flight;
-     kind 3 / 4 / 5 / 6: read / write / copy / update dst in place; grid x 1024
-       threads, workgroup w streams the w-th of grid contiguous spans, 8
-       accesses in flight;
-     kind 7: the momentum pack's three streams over spans: per 16-B gradient
-       unit read from src's first half, two 16-B momentum units of dst read and
-       rewritten and one 16-B unit written to src's second half (3 x bytes
-       moved), two gradient units in flight per thread.
-   No counterpart in the reference: it measures the bandwidth this GPU sustains,
-   the ceiling of the step's HBM-bound kernels (momentum pack, AdamW).  bytes a
-   positive multiple of 32, buffers 16-B aligned; the read probes may pass
-   dst = NULL (else dst holds grid * 4096 (kind 0) or grid * 16384 (kind 3)
-   bytes). */
-int mmuon_hbm_stream(int32_t kind, void* dst, void* src, int64_t bytes, int32_t nontemporal,
-                     int32_t grid, void* stream);
 
 /* Thread-local message of the last failing call ("" if none). */
 const char* mmuon_last_error(void);

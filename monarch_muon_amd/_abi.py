@@ -13,25 +13,27 @@ import torch
 
 LIB_PATH = Path(os.environ.get("MMUON_LIB", Path(__file__).resolve().parent / "libmmuon.so"))
 
-F32, BF16, F8E4M3 = 0, 1, 2
+F32, BF16, F8E4M3, F8E5M2 = 0, 1, 2, 3
 GROUP_ALIGNED16 = 1
 NS_NO_APPLY = 1
 NS_STANDARD = 2
 NS_HOLD_LAST = 4
-ABI_VERSION = 6
+ABI_VERSION = 7
 # Newton-Schulz plan ops (MMUON_NSOP_*) and buffers (MMUON_NSB_*)
 NSOP_SYRK, NSOP_POLY, NSOP_PX, NSOP_PX_APPLY, NSOP_SYMM = 0, 1, 2, 3, 4
 NSB_X0, NSB_X1, NSB_A, NSB_P, NSB_X0_S0, NSB_X0_S1, NSB_X1_S0, NSB_X1_S1, NSB_PARAM = range(9)
 NOALLOC_SCRATCH_FLOATS = 1 << 20
 
-_DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8E4M3}
+_DTYPES = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: F8E4M3, torch.float8_e5m2: F8E5M2}
+FP8_DTYPES = (torch.float8_e4m3fn, torch.float8_e5m2)
 
 
 def dtype_code(dt: torch.dtype) -> int:
     try:
         return _DTYPES[dt]
     except KeyError:
-        raise TypeError(f"libmmuon supports float32, bfloat16 and float8_e4m3fn tensors, not {dt}") from None
+        raise TypeError(f"libmmuon supports float32, bfloat16, float8_e4m3fn and float8_e5m2 tensors, "
+                        f"not {dt}") from None
 
 
 class BlockRef(C.Structure):
@@ -107,7 +109,7 @@ SIGNATURES = {
     "mmuon_last_error": (C.c_char_p, []),
     "mmuon_ns_layout": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int64, C.POINTER(NsLayout)]),
     "mmuon_momentum_pack": (C.c_int, [C.POINTER(Group), C.c_float, C.c_void_p]),
-    "mmuon_fp8_momentum_pack": (C.c_int, [C.POINTER(Group), C.c_float, C.c_int32, C.c_void_p]),
+    "mmuon_fp8_momentum_pack": (C.c_int, [C.POINTER(Group), C.c_float, C.c_int32, C.c_float, C.c_void_p]),
     "mmuon_newton_schulz_apply": (C.c_int, [C.POINTER(Group), C.c_int32, C.POINTER(C.c_float),
                                             C.c_float, C.c_int32, C.c_void_p]),
     "mmuon_ns_stage": (C.c_int, [C.POINTER(Group), C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_float),
@@ -117,19 +119,17 @@ SIGNATURES = {
     "mmuon_ns_run_op": (C.c_int, [C.POINTER(Group), C.POINTER(NsOp), C.POINTER(C.c_float), C.c_float,
                                   C.c_void_p]),
     "mmuon_adamw": (C.c_int, [C.POINTER(AdamWArgs), C.c_void_p]),
-    "mmuon_adamw_fp8": (C.c_int, [C.POINTER(AdamWArgs), C.POINTER(AdamWFp8Tensor), C.c_int32,
-                                  C.c_void_p]),
+    "mmuon_adamw_fp8": (C.c_int, [C.POINTER(AdamWArgs), C.POINTER(AdamWFp8Tensor), C.c_int32, C.c_int32,
+                                  C.c_float, C.c_void_p]),
     "mmuon_fp8_quantize": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
-                                     C.c_int64, C.c_int32, C.c_void_p]),
+                                     C.c_int64, C.c_int32, C.c_int32, C.c_float, C.c_void_p]),
     "mmuon_fp8_dequantize": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
-                                       C.c_int64, C.c_int32, C.c_void_p]),
+                                       C.c_int64, C.c_int32, C.c_int32, C.c_void_p]),
     "mmuon_grad_clip_coef": (C.c_int, [C.POINTER(GradNormArgs), C.c_void_p]),
     "mmuon_grad_clip_coef_noalloc": (C.c_int, [C.POINTER(GradNormArgs), C.c_void_p]),
     "mmuon_butterfly_fwd": (C.c_int, [C.POINTER(ButterflyArgs), C.c_void_p]),
     "mmuon_butterfly_bwd": (C.c_int, [C.POINTER(ButterflyArgs), C.c_void_p]),
     "mmuon_butterfly_workspace": (C.c_size_t, [C.POINTER(ButterflyArgs)]),
-    "mmuon_hbm_stream": (C.c_int, [C.c_int32, C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_int32,
-                                   C.c_void_p]),
 }
 
 _lib = None
@@ -189,27 +189,31 @@ def ns_output_buffer(rows: int, cols: int, ns_dtype: int, iters: int, flags: int
 
 
 def fp8_quantize(value: torch.Tensor, codes: torch.Tensor, scale: torch.Tensor, expand: torch.Tensor,
-                 sqrt_minmax: torch.Tensor, signed: bool) -> None:
-    """Stand-alone codec: fp32 ``value`` -> e4m3 ``codes`` + per-128 metadata (in place)."""
+                 sqrt_minmax: torch.Tensor, signed: bool, fmt: torch.dtype = torch.float8_e4m3fn,
+                 expand_min: float = 16) -> None:
+    """Stand-alone codec: fp32 ``value`` -> FP8 ``codes`` (``fmt``: float8_e4m3fn
+    or float8_e5m2; a uint8 ``codes`` tensor holds the raw bytes) + per-128
+    metadata (in place)."""
     _require_cuda(value, codes, scale, expand, sqrt_minmax)
     assert value.dtype == torch.float32 and value.is_contiguous()
-    assert codes.dtype in (torch.uint8, torch.float8_e4m3fn) and codes.is_contiguous()
+    assert codes.dtype in (torch.uint8, fmt) and codes.is_contiguous() and codes.numel() == value.numel()
     groups = (value.numel() + 127) // 128
     for t in (scale, expand, sqrt_minmax):
         assert t.dtype == torch.float32 and t.numel() >= groups and t.is_contiguous()
     check(lib().mmuon_fp8_quantize(value.data_ptr(), codes.data_ptr(), scale.data_ptr(), expand.data_ptr(),
-                                   sqrt_minmax.data_ptr(), value.numel(), int(signed),
-                                   stream_handle(value.device)), "mmuon_fp8_quantize")
+                                   sqrt_minmax.data_ptr(), value.numel(), int(signed), dtype_code(fmt),
+                                   float(expand_min), stream_handle(value.device)), "mmuon_fp8_quantize")
 
 
 def fp8_dequantize(codes: torch.Tensor, scale: torch.Tensor, expand: torch.Tensor,
-                   sqrt_minmax: torch.Tensor, out: torch.Tensor, signed: bool) -> None:
+                   sqrt_minmax: torch.Tensor, out: torch.Tensor, signed: bool,
+                   fmt: torch.dtype = torch.float8_e4m3fn) -> None:
     _require_cuda(codes, scale, expand, sqrt_minmax, out)
     assert out.dtype == torch.float32 and out.is_contiguous() and codes.is_contiguous()
-    assert out.numel() == codes.numel()
+    assert codes.dtype in (torch.uint8, fmt) and out.numel() == codes.numel()
     check(lib().mmuon_fp8_dequantize(codes.data_ptr(), scale.data_ptr(), expand.data_ptr(),
                                      sqrt_minmax.data_ptr(), out.data_ptr(), out.numel(), int(signed),
-                                     stream_handle(out.device)), "mmuon_fp8_dequantize")
+                                     dtype_code(fmt), stream_handle(out.device)), "mmuon_fp8_dequantize")
 
 
 def _require_cuda(*ts: torch.Tensor) -> None:

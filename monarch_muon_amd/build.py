@@ -2,7 +2,9 @@
 
 ``python -m monarch_muon_amd.build`` compiles every ``csrc/*.hip`` to an object
 in parallel and links the shared library next to this file.  hipcc
-cross-compiles for gfx950 without a GPU.
+cross-compiles for gfx950 without a GPU.  ``build_probe()`` builds the
+bench-only HBM streaming probe (``bench_probe.hip`` beside ``bench.py``) into a
+library of its own, apart from the optimizer's.
 """
 from __future__ import annotations
 
@@ -62,6 +64,23 @@ def build(verbose: bool = True) -> Path:
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources", file=sys.stderr)
     return LIB
+
+
+def build_probe(verbose: bool = True) -> Path:
+    """``bench_probe.so`` from ``bench_probe.hip`` at the repository root (used
+    only by ``bench.py --hbm-ceiling`` / ``--data-energy``)."""
+    root = HERE.parent
+    src, out = root / "bench_probe.hip", root / "bench_probe.so"
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [_hipcc(), *CFLAGS, "-shared", f"-I{root}", str(src), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        msg = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l)
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{msg}")
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}", file=sys.stderr)
+    return out
 
 
 if __name__ == "__main__":

@@ -42,8 +42,17 @@ int dtype_size(int dt) {
     case MMUON_F32: return 4;
     case MMUON_BF16: return 2;
     case MMUON_F8E4M3: return 1;
+    case MMUON_F8E5M2: return 1;
   }
   return 0;
+}
+
+bool is_fp8(int dt) { return dt == MMUON_F8E4M3 || dt == MMUON_F8E5M2; }
+
+// expand_min of the FP8 codec: a positive finite number
+int check_expand_min(float e) {
+  if (!(e > 0.f) || !(e <= 3.4e38f)) return fail(MMUON_EINVAL, "expand_min must be positive and finite (got %g)", e);
+  return MMUON_OK;
 }
 
 struct Geometry {
@@ -130,7 +139,7 @@ extern "C" {
 
 const char* mmuon_last_error(void) { return g_err.c_str(); }
 
-int mmuon_abi_version(void) { return 6; }
+int mmuon_abi_version(void) { return 7; }
 
 int mmuon_ns_layout(int32_t rows, int32_t cols, int32_t ns_dtype, int64_t nblocks,
                     mmuon_ns_layout_t* out) {
@@ -168,18 +177,20 @@ int mmuon_momentum_pack(const mmuon_group* g, float momentum, void* stream) {
   return check_launch("mmuon_momentum_pack");
 }
 
-int mmuon_fp8_momentum_pack(const mmuon_group* g, float momentum, int32_t have_state, void* stream) {
+int mmuon_fp8_momentum_pack(const mmuon_group* g, float momentum, int32_t have_state, float expand_min,
+                            void* stream) {
   Geometry geo;
   if (int rc = check_group(g, geo)) return rc;
-  if (g->buf_dtype != MMUON_F8E4M3) return fail(MMUON_EINVAL, "buf dtype must be MMUON_F8E4M3");
+  if (!is_fp8(g->buf_dtype)) return fail(MMUON_EINVAL, "buf dtype must be MMUON_F8E4M3 or MMUON_F8E5M2");
+  if (int rc = check_expand_min(expand_min)) return rc;
   if (g->fp8 == nullptr) return fail(MMUON_EINVAL, "null FP8 metadata table");
   if ((int64_t(g->rows) * g->cols) % 128 != 0)
     return fail(MMUON_EINVAL, "FP8 momentum needs rows*cols %% 128 == 0 (got %d x %d)", g->rows, g->cols);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const int nparts = mmuon::fp8_pack_nparts(g->rows, g->cols, geo.transposed);
   mmuon::PackArgs a = pack_args(g, geo, momentum, nparts);
-  if (mmuon::launch_fp8_pack(a, g->fp8, g->rows, g->cols, g->grad_dtype, g->ns_dtype, geo.transposed,
-                             have_state ? 1 : 0, s))
+  if (mmuon::launch_fp8_pack(a, g->fp8, g->rows, g->cols, g->grad_dtype, g->ns_dtype, g->buf_dtype,
+                             geo.transposed, have_state ? 1 : 0, expand_min, s))
     return fail(MMUON_EINVAL, "unsupported dtype combination grad=%d ns=%d", g->grad_dtype, g->ns_dtype);
   mmuon::launch_block_scale(g->partial, nparts, g->scale, g->nblocks, g->ns_dtype == MMUON_BF16, s);
   return check_launch("mmuon_fp8_momentum_pack");
@@ -465,38 +476,45 @@ int mmuon_adamw(const mmuon_adamw_args* a, void* stream) {
 }
 
 int mmuon_adamw_fp8(const mmuon_adamw_args* a, const mmuon_adamw_fp8_tensor* meta, int32_t have_state,
-                    void* stream) {
+                    int32_t v_dtype, float expand_min, void* stream) {
   if (int rc = check_adamw(a)) return rc;
   if (a->chunk_elems != 128) return fail(MMUON_EINVAL, "FP8 AdamW needs chunk_elems == 128");
-  if (a->state_dtype != MMUON_F8E4M3) return fail(MMUON_EINVAL, "FP8 AdamW needs state dtype F8E4M3");
+  if (!is_fp8(a->state_dtype) || !is_fp8(v_dtype))
+    return fail(MMUON_EINVAL, "FP8 AdamW needs F8E4M3 or F8E5M2 states (got %d, %d)", a->state_dtype, v_dtype);
+  if (int rc = check_expand_min(expand_min)) return rc;
   if (a->nchunks > 0 && meta == nullptr) return fail(MMUON_EINVAL, "null FP8 metadata table");
   mmuon::AdamWArgs k = adamw_args(a);
   k.fp8 = meta;
   k.have_state = have_state ? 1 : 0;
-  if (mmuon::launch_adamw_fp8(k, a->param_dtype, a->grad_dtype, static_cast<hipStream_t>(stream)))
+  k.emin = expand_min;
+  if (mmuon::launch_adamw_fp8(k, a->param_dtype, a->grad_dtype, a->state_dtype, v_dtype,
+                              static_cast<hipStream_t>(stream)))
     return fail(MMUON_EINVAL, "unsupported FP8 AdamW dtypes param=%d grad=%d", a->param_dtype, a->grad_dtype);
   return check_launch("mmuon_adamw_fp8");
 }
 
 int mmuon_fp8_quantize(const float* value, uint8_t* codes, float* scale, float* expand, float* sqrt_minmax,
-                       int64_t numel, int32_t signed_, void* stream) {
+                       int64_t numel, int32_t signed_, int32_t fp8_dtype, float expand_min, void* stream) {
   if (numel < 0) return fail(MMUON_EINVAL, "negative numel");
   if (numel > 0 && (!value || !codes || !scale || !expand || !sqrt_minmax))
     return fail(MMUON_EINVAL, "null codec pointer");
-  if ((numel + 127) / 128 / 4 > 0x7fffffff) return fail(MMUON_ERANGE, "tensor too large");
-  mmuon::launch_fp8_quantize(value, codes, scale, expand, sqrt_minmax, numel, signed_ != 0,
+  if (!is_fp8(fp8_dtype)) return fail(MMUON_EINVAL, "fp8_dtype must be MMUON_F8E4M3 or MMUON_F8E5M2");
+  if (int rc = check_expand_min(expand_min)) return rc;
+  if ((numel + 127) / 128 / 32 > 0x7fffffff) return fail(MMUON_ERANGE, "tensor too large");
+  mmuon::launch_fp8_quantize(value, codes, scale, expand, sqrt_minmax, numel, signed_ != 0, fp8_dtype, expand_min,
                              static_cast<hipStream_t>(stream));
   return check_launch("mmuon_fp8_quantize");
 }
 
 int mmuon_fp8_dequantize(const uint8_t* codes, const float* scale, const float* expand,
                          const float* sqrt_minmax, float* out, int64_t numel, int32_t signed_,
-                         void* stream) {
+                         int32_t fp8_dtype, void* stream) {
   if (numel < 0) return fail(MMUON_EINVAL, "negative numel");
   if (numel > 0 && (!out || !codes || !scale || !expand || !sqrt_minmax))
     return fail(MMUON_EINVAL, "null codec pointer");
-  if (numel / 256 > 0x7fffffff) return fail(MMUON_ERANGE, "tensor too large");
-  mmuon::launch_fp8_dequantize(codes, scale, expand, sqrt_minmax, out, numel, signed_ != 0,
+  if (!is_fp8(fp8_dtype)) return fail(MMUON_EINVAL, "fp8_dtype must be MMUON_F8E4M3 or MMUON_F8E5M2");
+  if ((numel + 127) / 128 / 32 > 0x7fffffff) return fail(MMUON_ERANGE, "tensor too large");
+  mmuon::launch_fp8_dequantize(codes, scale, expand, sqrt_minmax, out, numel, signed_ != 0, fp8_dtype,
                                static_cast<hipStream_t>(stream));
   return check_launch("mmuon_fp8_dequantize");
 }

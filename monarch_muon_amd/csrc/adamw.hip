@@ -102,14 +102,18 @@ int launch_adamw(const AdamWArgs& a, int param_dtype, int grad_dtype, int state_
 }
 
 // ---------------------------------------------------------------------------
-// FP8-state AdamW: one 128-element metadata group per F8_LANES lanes,
-// F8_ELEMS (16) consecutive elements per lane; the moments are dequantized to fp32,
+// FP8-state AdamW: one 128-element metadata group per F8_LANES (8) lanes,
+// F8_ELEMS (16) consecutive elements per lane (32 per lane, which shares each
+// group's metadata work among more elements, takes 190 VGPRs, two waves per
+// SIMD, and measured 5% slower); the moments are dequantized to fp32,
 // updated in fp32 (the reference's dequantized states are fp32 tensors), and
-// requantized (exp_avg signed, exp_avg_sq unsigned).  Moments created in this
-// step (have_state 0) start at zero in the parameter dtype and every moment op
-// rounds to it (TS = TP), as the wrapped step's zeros_like(param) states do
-// (coat_state_muon.py:126-139 around membench monarch_muon.py:184-190).
-// chunk = tensor << 40 | first element of the group.
+// requantized (exp_avg signed in format FM, exp_avg_sq unsigned in format FV:
+// the reference's first_order_bit / second_order_bit, coat_state_muon.py:121-122).
+// Moments created in this step (have_state 0) start at zero in the parameter
+// dtype and every moment op rounds to it (TS = TP), as the wrapped step's
+// zeros_like(param) states do (coat_state_muon.py:126-139 around membench
+// monarch_muon.py:184-190).  chunk = tensor << 40 | first element of the group;
+// a tensor's last group may be short (numel % 128 != 0).
 // ---------------------------------------------------------------------------
 constexpr int F8_ELEMS = 16, F8_LANES = 128 / F8_ELEMS;
 constexpr int F8_GPW = ADAM_NT / F8_LANES;  // groups per workgroup
@@ -118,33 +122,43 @@ template <class T>
 __device__ __forceinline__ void load_lane(const typename T::storage* p, int64_t e0, int nvalid, bool vec,
                                           float v[F8_ELEMS]) {
   if (vec) {
-    Vec8<T>::load(p + e0, v);
-    Vec8<T>::load(p + e0 + 8, v + 8);
+#pragma unroll
+    for (int h = 0; h < F8_ELEMS / 8; ++h) Vec8<T>::load(p + e0 + 8 * h, v + 8 * h);
     return;
   }
 #pragma unroll
   for (int k = 0; k < F8_ELEMS; ++k) v[k] = k < nvalid ? T::load(p, e0 + k) : 0.f;
 }
-__device__ __forceinline__ uint4 load_codes(const uint8_t* q, int64_t e0, int nvalid, bool vec) {
-  if (vec) return *reinterpret_cast<const uint4*>(q + e0);
-  uint32_t w[4] = {0u, 0u, 0u, 0u};
+__device__ __forceinline__ void load_codes(const uint8_t* q, int64_t e0, int nvalid, bool vec,
+                                           uint4 (&c)[F8_ELEMS / 16]) {
+  if (vec) {
+#pragma unroll
+    for (int h = 0; h < F8_ELEMS / 16; ++h) c[h] = *reinterpret_cast<const uint4*>(q + e0 + 16 * h);
+    return;
+  }
+  uint32_t w[F8_ELEMS / 4] = {};
 #pragma unroll
   for (int k = 0; k < F8_ELEMS; ++k)
     if (k < nvalid) w[k >> 2] |= uint32_t(q[e0 + k]) << (8 * (k & 3));
-  return make_uint4(w[0], w[1], w[2], w[3]);
+#pragma unroll
+  for (int h = 0; h < F8_ELEMS / 16; ++h) c[h] = make_uint4(w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]);
 }
-__device__ __forceinline__ void store_codes(uint8_t* q, int64_t e0, int nvalid, bool vec, uint4 c) {
+__device__ __forceinline__ void store_codes(uint8_t* q, int64_t e0, int nvalid, bool vec,
+                                            const uint4 (&c)[F8_ELEMS / 16]) {
   if (vec) {
-    *reinterpret_cast<uint4*>(q + e0) = c;
+#pragma unroll
+    for (int h = 0; h < F8_ELEMS / 16; ++h) *reinterpret_cast<uint4*>(q + e0 + 16 * h) = c[h];
     return;
   }
-  const uint32_t w[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
-  for (int k = 0; k < F8_ELEMS; ++k)
-    if (k < nvalid) q[e0 + k] = uint8_t(w[k >> 2] >> (8 * (k & 3)));
+  for (int k = 0; k < F8_ELEMS; ++k) {
+    const uint4& u = c[k >> 4];
+    const uint32_t w = (k & 15) < 4 ? u.x : (k & 15) < 8 ? u.y : (k & 15) < 12 ? u.z : u.w;
+    if (k < nvalid) q[e0 + k] = uint8_t(w >> (8 * (k & 3)));
+  }
 }
 
-template <class TP, class TG, class TS>
+template <class TP, class TG, class TS, class FM, class FV>
 __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
   const int64_t gidx = int64_t(blockIdx.x) * F8_GPW + (threadIdx.x / F8_LANES);
   if (gidx >= a.nchunks) return;  // a group's lanes leave together
@@ -161,35 +175,43 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
   uint8_t* qv = reinterpret_cast<uint8_t*>(T.exp_avg_sq);
   const int64_t e0 = start + sub * F8_ELEMS;
   const int nvalid = int(max(int64_t(0), min(int64_t(F8_ELEMS), T.numel - e0)));
+  const bool full = start + 128 <= T.numel;  // uniform over the group's lanes
   // 16-B parameter / gradient / code accesses for a full, aligned lane
   const uintptr_t al = reinterpret_cast<uintptr_t>(p + e0) | reinterpret_cast<uintptr_t>(g + e0) |
                        reinterpret_cast<uintptr_t>(qm + e0) | reinterpret_cast<uintptr_t>(qv + e0);
   const bool vec = nvalid == F8_ELEMS && (al & 15) == 0;
   float pv[F8_ELEMS], gv[F8_ELEMS], m[F8_ELEMS], v[F8_ELEMS];
-#pragma unroll
-  for (int k = 0; k < F8_ELEMS; ++k) m[k] = v[k] = 0.f;
   load_lane<TP>(p, e0, nvalid, vec, pv);
   load_lane<TG>(g, e0, nvalid, vec, gv);
   if (a.have_state) {
-    const uint4 cm[1] = {load_codes(qm, e0, nvalid, vec)}, cv[1] = {load_codes(qv, e0, nvalid, vec)};
-    fp8_dequant_lane<F8_ELEMS>(cm, fp8_dq(Fp8Meta{M.scale_m[grp], M.expand_m[grp], M.sqrt_minmax_m[grp]}), true, m);
-    fp8_dequant_lane<F8_ELEMS>(cv, fp8_dq(Fp8Meta{M.scale_v[grp], M.expand_v[grp], M.sqrt_minmax_v[grp]}), false, v);
+    uint4 cm[F8_ELEMS / 16], cv[F8_ELEMS / 16];
+    load_codes(qm, e0, nvalid, vec, cm);
+    load_codes(qv, e0, nvalid, vec, cv);
+    fp8_dequant_lane<FM, F8_ELEMS>(cm, fp8_dq<FM>(Fp8Meta{M.scale_m[grp], M.expand_m[grp], M.sqrt_minmax_m[grp]}),
+                                   true, m);
+    fp8_dequant_lane<FV, F8_ELEMS>(cv, fp8_dq<FV>(Fp8Meta{M.scale_v[grp], M.expand_v[grp], M.sqrt_minmax_v[grp]}),
+                                   false, v);
+  } else {
+#pragma unroll
+    for (int k = 0; k < F8_ELEMS; ++k) m[k] = v[k] = 0.f;
   }
 #pragma unroll
   for (int k = 0; k < F8_ELEMS; ++k) adamw_elem<TP, TS>(pv[k], clipped<TG>(gv[k], a.gscale), m[k], v[k], a);
   if (vec) {
-    Vec8<TP>::store(p + e0, pv);
-    Vec8<TP>::store(p + e0 + 8, pv + 8);
+#pragma unroll
+    for (int h = 0; h < F8_ELEMS / 8; ++h) Vec8<TP>::store(p + e0 + 8 * h, pv + 8 * h);
   } else {
 #pragma unroll
     for (int k = 0; k < F8_ELEMS; ++k)
       if (k < nvalid) TP::store(p, e0 + k, pv[k]);
   }
-  uint4 c[1];
-  const Fp8Meta nm = fp8_quant_group<F8_ELEMS>(m, nvalid, true, c);
-  store_codes(qm, e0, nvalid, vec, c[0]);
-  const Fp8Meta nv = fp8_quant_group<F8_ELEMS>(v, nvalid, false, c);
-  store_codes(qv, e0, nvalid, vec, c[0]);
+  uint4 c[F8_ELEMS / 16];
+  const Fp8Meta nm = full ? fp8_quant_group<FM, F8_ELEMS, true>(m, F8_ELEMS, true, a.emin, c)
+                          : fp8_quant_group<FM, F8_ELEMS, false>(m, nvalid, true, a.emin, c);
+  store_codes(qm, e0, nvalid, vec, c);
+  const Fp8Meta nv = full ? fp8_quant_group<FV, F8_ELEMS, true>(v, F8_ELEMS, false, a.emin, c)
+                          : fp8_quant_group<FV, F8_ELEMS, false>(v, nvalid, false, a.emin, c);
+  store_codes(qv, e0, nvalid, vec, c);
   if (sub == 0) {
     M.scale_m[grp] = nm.scale;
     M.expand_m[grp] = nm.expand;
@@ -200,18 +222,29 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
   }
 }
 
-int launch_adamw_fp8(const AdamWArgs& a, int param_dtype, int grad_dtype, hipStream_t s) {
-  if (a.nchunks <= 0) return 0;
+template <class FM, class FV>
+static int launch_adamw_fp8_f(const AdamWArgs& a, int param_dtype, int grad_dtype, hipStream_t s) {
   const dim3 grid(unsigned((a.nchunks + F8_GPW - 1) / F8_GPW)), block(ADAM_NT);
   if (param_dtype == MMUON_BF16 && grad_dtype == MMUON_BF16) {
-    if (a.have_state) hipLaunchKernelGGL((adamw_fp8_kernel<BF16T, BF16T, F32T>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((adamw_fp8_kernel<BF16T, BF16T, BF16T>), grid, block, 0, s, a);
+    if (a.have_state) hipLaunchKernelGGL((adamw_fp8_kernel<BF16T, BF16T, F32T, FM, FV>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((adamw_fp8_kernel<BF16T, BF16T, BF16T, FM, FV>), grid, block, 0, s, a);
   } else if (param_dtype == MMUON_F32 && grad_dtype == MMUON_F32) {
-    hipLaunchKernelGGL((adamw_fp8_kernel<F32T, F32T, F32T>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((adamw_fp8_kernel<F32T, F32T, F32T, FM, FV>), grid, block, 0, s, a);
   } else {
     return -1;
   }
   return 0;
+}
+
+int launch_adamw_fp8(const AdamWArgs& a, int param_dtype, int grad_dtype, int m_dtype, int v_dtype, hipStream_t s) {
+  if (a.nchunks <= 0) return 0;
+  const bool m8 = m_dtype == MMUON_F8E4M3, m5 = m_dtype == MMUON_F8E5M2;
+  const bool v8 = v_dtype == MMUON_F8E4M3, v5 = v_dtype == MMUON_F8E5M2;
+  if (m8 && v8) return launch_adamw_fp8_f<E4M3, E4M3>(a, param_dtype, grad_dtype, s);
+  if (m8 && v5) return launch_adamw_fp8_f<E4M3, E5M2>(a, param_dtype, grad_dtype, s);
+  if (m5 && v8) return launch_adamw_fp8_f<E5M2, E4M3>(a, param_dtype, grad_dtype, s);
+  if (m5 && v5) return launch_adamw_fp8_f<E5M2, E5M2>(a, param_dtype, grad_dtype, s);
+  return -1;
 }
 
 }  // namespace mmuon

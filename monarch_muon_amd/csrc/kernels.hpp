@@ -65,11 +65,12 @@ struct AdamWArgs {
   float neg_step_size;  // -lr / (1 - beta1^t)
   const mmuon_adamw_fp8_tensor* fp8;
   int have_state;
+  float emin;           // FP8 states: expand_min of the codec
   const float* gscale;  // gradient-clipping coefficient (device), or null
 };
 int launch_adamw(const AdamWArgs& a, int param_dtype, int grad_dtype, int state_dtype,
                  hipStream_t s);
-int launch_adamw_fp8(const AdamWArgs& a, int param_dtype, int grad_dtype, hipStream_t s);
+int launch_adamw_fp8(const AdamWArgs& a, int param_dtype, int grad_dtype, int m_dtype, int v_dtype, hipStream_t s);
 
 // Gradient-norm clipping coefficient --------------------------------------------
 int launch_grad_clip_coef(const mmuon_grad_norm_args& a, hipStream_t s);
@@ -93,14 +94,13 @@ __device__ __forceinline__ float clipped(float g, const float* gscale) {
   return gscale != nullptr ? TG::round(g * *gscale) : g;
 }
 
-// FP8 codec -------------------------------------------------------------------
-void launch_fp8_quantize(const float* v, uint8_t* q, float* sc, float* ex, float* smm,
-                         int64_t numel, bool sgn, hipStream_t s);
-void launch_fp8_dequantize(const uint8_t* q, const float* sc, const float* ex, const float* smm,
-                           float* out, int64_t numel, bool sgn, hipStream_t s);
+// FP8 codec (fp8_dtype: MMUON_F8E4M3 or MMUON_F8E5M2; emin: expand_min) -------
+int launch_fp8_quantize(const float* v, uint8_t* q, float* sc, float* ex, float* smm, int64_t numel, bool sgn,
+                        int fp8_dtype, float emin, hipStream_t s);
+int launch_fp8_dequantize(const uint8_t* q, const float* sc, const float* ex, const float* smm, float* out,
+                          int64_t numel, bool sgn, int fp8_dtype, hipStream_t s);
 int fp8_pack_nparts(int rows, int cols, bool transposed);
-int launch_fp8_pack(const PackArgs& a, const mmuon_block_fp8* meta, int rows, int cols,
-                    int grad_dtype, int x_dtype, bool transposed, int have_state,
-                    hipStream_t s);
+int launch_fp8_pack(const PackArgs& a, const mmuon_block_fp8* meta, int rows, int cols, int grad_dtype, int x_dtype,
+                    int fp8_dtype, bool transposed, int have_state, float emin, hipStream_t s);
 
 }  // namespace mmuon

@@ -231,7 +231,8 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
         stream = _abi.stream_handle(al.tensors.device)
         if al.fp8 is not None:
             _abi.check(lib.mmuon_adamw_fp8(C.byref(args), C.cast(al.fp8.data_ptr(), C.POINTER(_abi.AdamWFp8Tensor)),
-                                           int(have_state), stream), "mmuon_adamw_fp8")
+                                           int(have_state), _abi.dtype_code(al.vd), float(self.expand_min), stream),
+                       "mmuon_adamw_fp8")
         else:
             _abi.check(lib.mmuon_adamw(C.byref(args), stream), "mmuon_adamw")
 
@@ -255,7 +256,8 @@ class MonarchMuonOptimizer(torch.optim.Optimizer):
 # FP8 optimizer states (coat_state_muon.py:117-151)
 # ---------------------------------------------------------------------------
 STATES = {"momentum_buffer": True, "exp_avg": True, "exp_avg_sq": False}   # name -> signed
-_FP8 = {"E4M3": torch.float8_e4m3fn}
+_FP8 = {"E4M3": torch.float8_e4m3fn, "E5M2": torch.float8_e5m2}          # coat_state_muon.py:17
+_META = ("scale", "expand", "sqrt_minmax")
 
 
 class QuantizationConfig:
@@ -273,9 +275,15 @@ class QuantizationConfig:
 
 
 class CoatStateMonarchMuon(MonarchMuonOptimizer):
-    """Every optimizer state stored as e4m3 in groups of 128 with dynamic range
-    expansion; each step dequantizes, updates and requantizes inside the fused
-    kernels (no fp32 copy of any state is materialised)."""
+    """Every optimizer state stored as FP8 (``first_order_bit`` for the momentum
+    and ``exp_avg``, ``second_order_bit`` for ``exp_avg_sq``: E4M3 or E5M2) in
+    groups of 128 of the flattened tensor with dynamic range expansion
+    (``expand_min``); each step dequantizes, updates and requantizes inside the
+    fused kernels.  A Monarch factor whose blocks hold a multiple of 128
+    elements is updated in place (no fp32 copy of the momentum); one whose
+    groups straddle its blocks takes the reference's own sequence over the
+    whole parameter: dequantize to a (cached) fp32 buffer, the plain step,
+    quantize back."""
 
     def __init__(self, *args, qargs, **kwargs):
         if qargs.qgroup_size != 128:
@@ -284,69 +292,116 @@ class CoatStateMonarchMuon(MonarchMuonOptimizer):
             raise AssertionError("only the dynamic-range-expansion codec is supported")
         for bit in (qargs.first_order_bit, qargs.second_order_bit):
             if bit not in _FP8:
-                raise NotImplementedError(f"FP8 state format {bit} (only E4M3 is implemented)")
-        if int(qargs.expand_min) != 16:
-            raise NotImplementedError("expand_min other than 16")
+                raise KeyError(f"FP8 state format {bit!r} (E4M3 or E5M2)")
+        emin = float(qargs.expand_min)
+        if not (emin > 0 and emin < float("inf")):
+            raise ValueError(f"expand_min must be positive (got {qargs.expand_min})")
         self.dtypes = {name: _FP8[qargs.first_order_bit] for name in ("momentum_buffer", "exp_avg")}
         self.dtypes["exp_avg_sq"] = _FP8[qargs.second_order_bit]
         self.expand_min = qargs.expand_min
+        self._ragged = {}   # parameter -> cached momentum buffer of the straddling-group path
         super().__init__(*args, **kwargs)
 
-    @staticmethod
-    def _ensure_fp8(state, name, like):
-        """FP8 payload + metadata for ``state[name]``; a missing state starts as
-        exact zeros (codes 0 decode to 0 whatever the metadata)."""
+    def _ensure_fp8(self, state, name, like):
+        """FP8 payload + metadata for ``state[name]`` in this optimizer's format;
+        a missing state starts as exact zeros (codes 0 decode to 0 whatever the
+        metadata)."""
+        fmt = self.dtypes[name]
         groups = (like.numel() + 127) // 128
         cur = state.get(name)
-        if cur is None or cur.dtype != torch.float8_e4m3fn:
-            if cur is None:
-                state[name] = torch.zeros(like.shape, dtype=torch.float8_e4m3fn, device=like.device)
-                for key in ("scale", "expand", "sqrt_minmax"):
-                    state[f"{key}_{name}"] = torch.ones(groups, dtype=torch.float32, device=like.device)
-            else:
-                # a floating state (e.g. restored without its FP8 dtype): quantize it
-                value = cur.detach().to(torch.float32).contiguous()
-                codes = torch.empty(like.shape, dtype=torch.float8_e4m3fn, device=like.device)
-                meta = [torch.empty(groups, dtype=torch.float32, device=like.device) for _ in range(3)]
-                _abi.fp8_quantize(value, codes.view(torch.uint8), *meta, signed=STATES[name])
-                state[name] = codes
-                for key, t in zip(("scale", "expand", "sqrt_minmax"), meta):
-                    state[f"{key}_{name}"] = t
-        for key in ("scale", "expand", "sqrt_minmax"):
+        if cur is None:
+            state[name] = torch.zeros(like.shape, dtype=fmt, device=like.device)
+            for key in _META:
+                state[f"{key}_{name}"] = torch.ones(groups, dtype=torch.float32, device=like.device)
+        for key in _META:
             t = state[f"{key}_{name}"]
             if t.dtype != torch.float32:
                 state[f"{key}_{name}"] = t.to(torch.float32)
+        cur = state[name]
+        if cur.dtype != fmt:
+            # a floating state (e.g. restored without its FP8 dtype), or codes of
+            # the other FP8 format: quantize its value in this format
+            if cur.dtype in _abi.FP8_DTYPES:
+                value = torch.empty(like.shape, dtype=torch.float32, device=like.device)
+                _abi.fp8_dequantize(cur.contiguous(), *self._meta(state, name), value, signed=STATES[name],
+                                    fmt=cur.dtype)
+            else:
+                value = cur.detach().to(torch.float32).contiguous()
+            codes = torch.empty(like.shape, dtype=fmt, device=like.device)
+            meta = [torch.empty(groups, dtype=torch.float32, device=like.device) for _ in range(3)]
+            _abi.fp8_quantize(value, codes, *meta, signed=STATES[name], fmt=fmt, expand_min=self.expand_min)
+            state[name] = codes
+            for key, t in zip(_META, meta):
+                state[f"{key}_{name}"] = t
         return state[name]
 
     def _meta(self, state, name):
-        return tuple(state[f"{key}_{name}"] for key in ("scale", "expand", "sqrt_minmax"))
+        return tuple(state[f"{key}_{name}"] for key in _META)
+
+    def _ragged_buffer(self, p, dtype, codes, meta, have_state):
+        """The momentum of a parameter whose 128-groups straddle its blocks, as
+        the wrapped step sees it (coat_state_muon.py:128-132): the dequantized
+        fp32 tensor, or zeros in the parameter dtype when the step creates it.
+        The buffer is kept between steps (same shape and dtype)."""
+        buf = self._ragged.get(p)
+        if buf is None or buf.dtype != dtype or buf.shape != p.shape:
+            buf = self._ragged[p] = torch.empty(p.shape, dtype=dtype, device=p.device)
+        if have_state:
+            _abi.fp8_dequantize(codes, *meta, buf, signed=True, fmt=codes.dtype)
+        else:
+            buf.zero_()
+        return buf
+
+    def release_workspace(self) -> None:
+        super().release_workspace()
+        self._ragged = {}
 
     def _muon_step(self, group: dict, lr: float) -> None:
         params, grads = self._muon_inputs(group)
         if not params:
             return
-        for p in params:
-            if p.dim() != 3 or (p.numel() // p.shape[0]) % 128 != 0:
-                raise NotImplementedError("FP8 momentum needs rows*cols % 128 == 0 for every Monarch block")
         # the wrapped step sees a dequantized (fp32) momentum, or one it creates
         # with zeros_like(param) in the parameter dtype on a parameter's first
         # step: that dtype keys the grouping and, with ns_dtype=None, is the
         # Newton-Schulz dtype
-        key_dtypes = [torch.float32 if "momentum_buffer" in self.state[p] else p.dtype for p in params]
-        bufs = [self._ensure_fp8(self.state[p], "momentum_buffer", p) for p in params]
-        meta = [self._meta(self.state[p], "momentum_buffer") for p in params]
-        self._muon_planner.plan(params, grads, bufs, self.ns_dtype, fp8_meta=meta, key_dtypes=key_dtypes)
+        name = "momentum_buffer"
+        have = ["momentum_buffer" in self.state[p] for p in params]
+        key_dtypes = [torch.float32 if h else p.dtype for p, h in zip(params, have)]
+        bufs, metas, ragged = [], [], []
+        for p, h, kd in zip(params, have, key_dtypes):
+            if p.dim() != 3:
+                raise ValueError(f"Muon parameters must be 3-D (nblocks, rows, cols); got shape {tuple(p.shape)}")
+            st = self.state[p]
+            codes = self._ensure_fp8(st, name, p)
+            if (p.shape[1] * p.shape[2]) % 128 == 0:
+                bufs.append(codes)
+                metas.append(self._meta(st, name))
+            else:
+                buf = self._ragged_buffer(p, kd, codes, self._meta(st, name), h)
+                bufs.append(buf)
+                metas.append(None)
+                ragged.append((p, buf))
+        self._muon_planner.plan(params, grads, bufs, self.ns_dtype, fp8_meta=metas, key_dtypes=key_dtypes)
         momentum = float(group["momentum"])
         lib = _abi.lib()
         gscale = self._grad_scale()
+        emin = float(self.expand_min)
 
         def pack(gl, stream):
             gl.struct.grad_scale = gscale
-            _abi.check(lib.mmuon_fp8_momentum_pack(C.byref(gl.struct), momentum, 1, stream),
-                       "mmuon_fp8_momentum_pack")
+            if gl.struct.buf_dtype in (_abi.F8E4M3, _abi.F8E5M2):
+                _abi.check(lib.mmuon_fp8_momentum_pack(C.byref(gl.struct), momentum, 1, emin, stream),
+                           "mmuon_fp8_momentum_pack")
+            else:
+                _abi.check(lib.mmuon_momentum_pack(C.byref(gl.struct), momentum, stream), "mmuon_momentum_pack")
 
         run_newton_schulz(self._muon_planner.units, lib, _COEFFS, lr, self._ns_flags, NS_STEPS,
                           lambda gl: _abi.stream_handle(gl.key[0]), pack)
+        for p, buf in ragged:   # quantize_ (coat_state_muon.py:134-138) over the whole parameter
+            st = self.state[p]
+            value = buf if buf.dtype == torch.float32 else buf.to(torch.float32)
+            _abi.fp8_quantize(value, st[name], *self._meta(st, name), signed=True, fmt=st[name].dtype,
+                              expand_min=self.expand_min)
 
     def _adamw_step(self, group: dict, lr: float) -> None:
         params = [p for p in group["params"] if p.grad is not None]
@@ -389,7 +444,7 @@ class CoatStateMonarchMuon(MonarchMuonOptimizer):
             entry = state_dict["state"][key]
             for name, dtype in dtypes.items():
                 state[name] = state[name].to(dtype)
-                for meta in ("scale", "expand", "sqrt_minmax"):
+                for meta in _META:
                     mk = f"{meta}_{name}"
                     if mk in entry:
                         # the saved fp32 metadata itself (torch's cast to a bf16

@@ -224,7 +224,9 @@ class MuonPlanner:
 
     @property
     def groups(self) -> list[GroupLaunch]:
-        """The reference's groups, in its order."""
+        """The reference's groups, in its order (a group whose parameters differ
+        in dtype appears as one entry per (param, grad) dtype pair, in order of
+        first appearance)."""
         return self._groups
 
     @property
@@ -242,14 +244,16 @@ class MuonPlanner:
         self._ws = {}
 
     def plan(self, params, grads, bufs, ns_dtype: torch.dtype, fp8_meta=None, key_dtypes=None) -> list[GroupLaunch]:
-        """Launch plan of one step.  ``key_dtypes`` (FP8 states): per parameter,
+        """Launch plan of one step.  ``fp8_meta`` (FP8 states): per parameter,
+        the (scale, expand, sqrt_minmax) tensors of an FP8 momentum buffer, or
+        None where its buffer is a plain one.  ``key_dtypes`` (FP8 states): per parameter,
         the dtype the wrapped reference step sees for its momentum -- fp32 once
         dequantized, the parameter dtype when the buffer is created in this
         step -- used for the grouping key and, with ``ns_dtype=None``, as the
         Newton-Schulz dtype."""
         sig = tuple((p.data_ptr(), b.data_ptr(), p.dtype, b.dtype, b.shape) for p, b in zip(params, bufs))
         if fp8_meta is not None:
-            sig = sig + tuple(t.data_ptr() for m in fp8_meta for t in m)
+            sig = sig + tuple(t.data_ptr() if m is not None else None for m in fp8_meta for t in (m or (None,)))
         if key_dtypes is not None:
             sig = sig + tuple(key_dtypes)
         gptr = [(g.data_ptr(), g.dtype) for g in grads]
@@ -259,8 +263,16 @@ class MuonPlanner:
             if self._regrad(params, grads, gptr):
                 return self._groups
         keys = bufs if key_dtypes is None else [_KeyView(b, d) for b, d in zip(bufs, key_dtypes)]
-        self._groups = [self._build(key, idx, params, grads, bufs, ns_dtype, fp8_meta)
-                        for key, idx in plan_groups(keys).items()]
+        self._groups = []
+        for key, idx in plan_groups(keys).items():
+            # the reference keys a group on its buffers alone and applies per
+            # parameter (membench :156, :165-170); parameters of one group whose
+            # (param, grad) dtypes differ get a launch group each, which share
+            # the group's Newton-Schulz launches (_link)
+            subs: "OrderedDict[tuple, list[int]]" = OrderedDict()
+            for i in idx:
+                subs.setdefault((params[i].dtype, grads[i].dtype), []).append(i)
+            self._groups += [self._build(key, sub, params, grads, bufs, ns_dtype, fp8_meta) for sub in subs.values()]
         self._link()
         self._sig, self._gptr = sig, gptr
         return self._groups
@@ -342,14 +354,14 @@ class MuonPlanner:
         for i in idx:
             p, g, b = params[i], grads[i], bufs[i]
             if p.dtype != pd or g.dtype != gd:
-                raise TypeError("parameters (and their grads) of one block shape must share a dtype")
+                raise TypeError("a launch group's parameters (and their grads) must share a dtype")
             if not (p.is_contiguous() and g.is_contiguous() and b.is_contiguous()):
                 raise ValueError("Muon parameters, grads and momentum buffers must be contiguous")
             if p.shape != b.shape or g.shape != p.shape:
                 raise ValueError("param, grad and momentum shapes differ")
         if ns_dtype is not None:
             ns_code = _abi.dtype_code(ns_dtype)
-        elif kdtype == torch.float8_e4m3fn:
+        elif kdtype in _abi.FP8_DTYPES:
             ns_code = _abi.F32          # the FP8 reference dequantizes the momentum to fp32
         else:
             ns_code = _abi.dtype_code(kdtype)
@@ -364,7 +376,9 @@ class MuonPlanner:
         aligned = not bool(np.any(rows_tab % 16))
         table = _h2d_int64(rows_tab, device)
         fp8_table = None
-        if fp8_meta is not None:
+        if fp8_meta is not None and bdtype in _abi.FP8_DTYPES:
+            if any(fp8_meta[i] is None for i in idx):
+                raise ValueError("FP8 momentum buffers need their metadata")
             mb = np.array([tuple(t.data_ptr() for t in fp8_meta[i]) for i in idx], dtype=np.int64)
             fp8_table = _h2d_int64(np.repeat(mb, counts, axis=0) + k[:, None] * (rc // 128 * 4), device)
         gl = GroupLaunch(key, rows, cols, nblocks, list(idx), None, table, fp8_table, rows_tab=rows_tab,
@@ -421,13 +435,14 @@ class AdamLaunch:
     members: list                 # indices into the step's param list
     pd: torch.dtype
     gd: torch.dtype
-    sd: torch.dtype
+    sd: torch.dtype               # exp_avg dtype
     tensors: torch.Tensor         # device int64 [T, 5]
     chunks: torch.Tensor          # device int64 [nchunks]
     nchunks: int
     chunk: int
     fp8: torch.Tensor | None = None  # device int64 [T, 6]
     host: np.ndarray | None = None   # host copy of `tensors`
+    vd: torch.dtype | None = None    # exp_avg_sq dtype (differs from sd only for FP8 states)
 
 
 class AdamPlanner:
@@ -445,7 +460,7 @@ class AdamPlanner:
         self._launches = []
 
     def plan(self, params, grads, ms, vs, fp8_meta=None) -> list[AdamLaunch]:
-        sig = tuple((p.data_ptr(), m.data_ptr(), v.data_ptr(), p.dtype, m.dtype, p.numel())
+        sig = tuple((p.data_ptr(), m.data_ptr(), v.data_ptr(), p.dtype, m.dtype, v.dtype, p.numel())
                     for p, m, v in zip(params, ms, vs))
         if fp8_meta is not None:
             sig = sig + tuple(t.data_ptr() for meta in fp8_meta for t in meta)
@@ -457,22 +472,22 @@ class AdamPlanner:
                 return self._launches
         buckets: "OrderedDict[tuple, list[int]]" = OrderedDict()
         for i, (p, g, m, v) in enumerate(zip(params, grads, ms, vs)):
-            if m.dtype != v.dtype:
+            if m.dtype != v.dtype and fp8_meta is None:
                 raise TypeError("exp_avg and exp_avg_sq must share a dtype")
             for t in (p, g, m, v):
                 if not t.is_contiguous():
                     raise ValueError("AdamW parameters, grads and states must be contiguous")
-            buckets.setdefault((p.device, p.dtype, g.dtype, m.dtype), []).append(i)
+            buckets.setdefault((p.device, p.dtype, g.dtype, m.dtype, v.dtype), []).append(i)
         launches = []
         chunk = 128 if fp8_meta is not None else ADAM_CHUNK
-        for (device, pd, gd, sd), idx in buckets.items():
+        for (device, pd, gd, sd, vd), idx in buckets.items():
             tens = np.array([(params[i].data_ptr(), grads[i].data_ptr(), ms[i].data_ptr(), vs[i].data_ptr(),
                               params[i].numel()) for i in idx], dtype=np.int64).reshape(-1, 5)
             chunks = _chunk_codes([params[i].numel() for i in idx], chunk)
             f8 = [tuple(x.data_ptr() for x in fp8_meta[i]) for i in idx] if fp8_meta is not None else None
             launches.append(AdamLaunch(
                 idx, pd, gd, sd, _h2d_int64(tens, device), _h2d_int64(chunks if chunks.size else [0], device),
-                int(chunks.size), chunk, _h2d_int64(f8, device) if f8 is not None else None, host=tens))
+                int(chunks.size), chunk, _h2d_int64(f8, device) if f8 is not None else None, host=tens, vd=vd))
         self._launches = launches
         self._sig, self._gptr = sig, gptr
         return launches

@@ -208,28 +208,33 @@ def newton_schulz_ortho(stack: torch.Tensor, ns_dtype=torch.bfloat16) -> torch.T
 # FP8 optimizer states (pretrain/src/models/monarch/coat_state_muon.py:117-139)
 # ---------------------------------------------------------------------------
 FP8_STATES = {"momentum_buffer": True, "exp_avg": True, "exp_avg_sq": False}   # name -> signed
+FP8_FORMATS = {torch.float8_e4m3fn: "E4M3", torch.float8_e5m2: "E5M2"}          # coat_state_muon.py:17
 
 
 def dequantize_state(state: dict, name: str, signed: bool) -> torch.Tensor:
-    """Restates ``dequantize`` (``coat_state_muon.py:94-100``): the e4m3 payload
-    ``state[name]`` and its per-128 metadata -> an fp32 tensor of the same shape
-    on the same device."""
+    """Restates ``dequantize`` (``coat_state_muon.py:94-100``): the FP8 payload
+    ``state[name]`` (e4m3fn or e5m2, decoded as its dtype) and its per-128
+    metadata -> an fp32 tensor of the same shape on the same device."""
     data = state[name]
     meta = [state[f"{key}_{name}"].detach().cpu().to(torch.float32).numpy() for key in ("scale", "expand",
                                                                                         "sqrt_minmax")]
     from . import codec
-    out = codec.dequantize(data.detach().cpu().view(torch.uint8).numpy().reshape(-1), *meta, signed)
+    out = codec.dequantize(data.detach().cpu().view(torch.uint8).numpy().reshape(-1), *meta, signed,
+                           FP8_FORMATS[data.dtype])
     return torch.from_numpy(out).reshape(data.shape).to(data.device)
 
 
-def quantize_state(state: dict, name: str, value: torch.Tensor, signed: bool) -> None:
+def quantize_state(state: dict, name: str, value: torch.Tensor, signed: bool,
+                   dtype: torch.dtype = torch.float8_e4m3fn, expand_min: float = 16) -> None:
     """Restates ``quantize_`` (``coat_state_muon.py:103-114``): store ``value``
-    (any float dtype; the kernel loads it as fp32) as e4m3 codes plus fp32
+    (any float dtype; the kernel loads it as fp32) as ``dtype`` codes (its
+    ``finfo.max`` is the codec's fp8_max) plus fp32
     ``scale_/expand_/sqrt_minmax_<name>``."""
     from . import codec
-    codes, scale, expand, smm = codec.quantize(value.detach().to(torch.float32).cpu().numpy().reshape(-1), signed)
+    codes, scale, expand, smm = codec.quantize(value.detach().to(torch.float32).cpu().numpy().reshape(-1), signed,
+                                               FP8_FORMATS[dtype], expand_min)
     dev = value.device
-    state[name] = torch.from_numpy(codes).view(torch.float8_e4m3fn).reshape(value.shape).to(dev)
+    state[name] = torch.from_numpy(codes).view(dtype).reshape(value.shape).to(dev)
     for key, t in zip(("scale", "expand", "sqrt_minmax"), (scale, expand, smm)):
         state[f"{key}_{name}"] = torch.from_numpy(t).to(dev)
 
@@ -248,6 +253,12 @@ class ReferenceCoatStateMonarchMuon(ReferenceMonarchMuon):
     the dequantized states are fp32."""
 
     keep_values = False   # tests: keep each state's value before it is quantized
+    # per state, the FP8 dtype it is stored in, and the codec's expand_min
+    # (coat_state_muon.py:121-123: first_order_bit for the momentum and exp_avg,
+    # second_order_bit for exp_avg_sq; COAT's defaults)
+    dtypes = {"momentum_buffer": torch.float8_e4m3fn, "exp_avg": torch.float8_e4m3fn,
+              "exp_avg_sq": torch.float8_e4m3fn}
+    expand_min = 16
 
     @torch.no_grad()
     def step(self, closure=None):
@@ -266,5 +277,5 @@ class ReferenceCoatStateMonarchMuon(ReferenceMonarchMuon):
                     value = state.pop(name)
                     if self.keep_values:
                         self.values.setdefault(p, {})[name] = value
-                    quantize_state(state, name, value, signed)
+                    quantize_state(state, name, value, signed, self.dtypes[name], self.expand_min)
         return loss

@@ -127,23 +127,27 @@ def test_butterfly_entry_points_validate_before_launching():
 
 
 def test_hbm_probe_validates_before_launching():
-    """mmuon_hbm_stream rejects every malformed request before it launches (no GPU needed)."""
-    lib = _abi.lib()
+    """The bench-only HBM probe (bench_probe.so, apart from libmmuon.so) rejects
+    every malformed request before it launches (no GPU needed); libmmuon.so
+    does not export it."""
+    import bench
+    lib = bench.probe_lib()
+    assert not hasattr(_abi.lib(), "mmuon_hbm_stream")
     n = 1 << 20
-    assert lib.mmuon_hbm_stream(8, 4096, 4096, n, 0, 16, None) == -1
-    assert b"kind" in lib.mmuon_last_error()
-    assert lib.mmuon_hbm_stream(2, 4096, 4096, n + 16, 0, 16, None) == -1   # not a multiple of 32
-    assert b"multiple of 32" in lib.mmuon_last_error()
-    assert lib.mmuon_hbm_stream(5, 4096, 4096, n, 0, 0, None) == -1
-    assert b"grid" in lib.mmuon_last_error()
+    assert lib.probe_hbm_stream(8, 4096, 4096, n, 0, 16, None) == -1
+    assert b"kind" in lib.probe_last_error()
+    assert lib.probe_hbm_stream(2, 4096, 4096, n + 16, 0, 16, None) == -1   # not a multiple of 32
+    assert b"multiple of 32" in lib.probe_last_error()
+    assert lib.probe_hbm_stream(5, 4096, 4096, n, 0, 0, None) == -1
+    assert b"grid" in lib.probe_last_error()
     for kind in (1, 2, 4, 5, 6, 7):      # every kind but the read probes needs dst
-        assert lib.mmuon_hbm_stream(kind, None, 4096, n, 0, 16, None) == -1
-        assert b"null" in lib.mmuon_last_error()
+        assert lib.probe_hbm_stream(kind, None, 4096, n, 0, 16, None) == -1
+        assert b"null" in lib.probe_last_error()
     for kind in (0, 2, 3, 5, 7):         # these read (kind 7 also writes) src
-        assert lib.mmuon_hbm_stream(kind, 4096, None, n, 0, 16, None) == -1
-    assert lib.mmuon_hbm_stream(6, 4100, 4096, n, 0, 16, None) == -1        # unaligned
-    assert b"aligned" in lib.mmuon_last_error()
+        assert lib.probe_hbm_stream(kind, 4096, None, n, 0, 16, None) == -1
+    assert lib.probe_hbm_stream(6, 4100, 4096, n, 0, 16, None) == -1        # unaligned
+    assert b"aligned" in lib.probe_last_error()
     # the read probes' guard store needs grid * 4096 (grid-stride) / grid * 16384 (spans) bytes of dst
-    assert lib.mmuon_hbm_stream(0, 4096, 4096, 4096 * 64, 0, 65, None) == -1
-    assert lib.mmuon_hbm_stream(3, 4096, 4096, 16384 * 16, 0, 17, None) == -1
-    assert b"read probe" in lib.mmuon_last_error()
+    assert lib.probe_hbm_stream(0, 4096, 4096, 4096 * 64, 0, 65, None) == -1
+    assert lib.probe_hbm_stream(3, 4096, 4096, 16384 * 16, 0, 17, None) == -1
+    assert b"read probe" in lib.probe_last_error()

@@ -235,3 +235,94 @@ def test_shared_newton_schulz_launches_equal_per_group_launches(name, fp8):
         for k in s1:
             if torch.is_tensor(s1[k]):
                 assert torch.equal(_bits(s1[k]), _bits(s2[k])), k
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["fp32mom", "fp8"])
+def test_steps_on_side_streams_equal_default_stream(fp8):
+    """The reference's benchmark harness builds its states and runs
+    ``optimizer.step()`` inside ``with torch.cuda.stream(stream)`` on a stream of
+    its own (``membench/scripts/monarch_benchmark/benchmark_train_step.py:285-299,
+    382``).  Here the optimizer is built and stepped on one side stream, the
+    next step runs on a second one and the third on the default stream (each
+    stream waiting on the previous one, as any program that moves work
+    between streams does); the planners' table uploads, workspaces and FP8
+    metadata follow the current stream.  The bits equal three steps on the
+    default stream."""
+    def run(streams):
+        muon, adamw = _layer("1.3b-nb4", seed=5)
+        prev = torch.cuda.current_stream()
+        opt = None
+        for s in streams:
+            s = s or torch.cuda.default_stream(DEV)
+            s.wait_stream(prev)
+            with torch.cuda.stream(s):
+                if opt is None:
+                    opt = (CoatStateMonarchMuon(muon, adamw, lr=0.02, momentum=0.95, qargs=QuantizationConfig())
+                           if fp8 else MonarchMuonOptimizer(muon, adamw, lr=0.02, momentum=0.95))
+                    if not fp8:
+                        gen = torch.Generator(device=DEV).manual_seed(9)
+                        for p in muon:
+                            opt.state[p]["momentum_buffer"] = torch.randn(p.shape, generator=gen, device=DEV) * 1e-3
+                for p in muon + adamw:   # the next step's gradients, written on this stream
+                    p.grad.mul_(1.25)
+                opt.step()
+            prev = s
+        torch.cuda.default_stream(DEV).wait_stream(prev)
+        torch.cuda.synchronize()
+        return muon + adamw, opt
+
+    s1, s2 = torch.cuda.Stream(DEV), torch.cuda.Stream(DEV)   # default priority
+    ref, ropt = run([None, None, None])
+    got, gopt = run([s1, s2, None])
+    for p, q in zip(ref, got):
+        assert torch.equal(p, q)
+        st1, st2 = ropt.state[p], gopt.state[q]
+        assert set(st1) == set(st2)
+        for k in st1:
+            if torch.is_tensor(st1[k]):
+                assert torch.equal(_bits(st1[k]), _bits(st2[k])), k
+
+
+def test_group_with_mixed_parameter_dtypes_matches_oracle():
+    """The reference keys its groups on the momentum buffer (device, dtype,
+    rows, cols) and applies the update per parameter (membench
+    ``monarch_muon.py:156,165-170``), so one group may hold bf16 and fp32
+    parameters whose buffers are both fp32.  Such a group gets one launch
+    group per (param, grad) dtype pair sharing its Newton-Schulz launches; the
+    step matches the oracle (weights within the bf16 bar, momentum bit for
+    bit)."""
+    from monarch_muon_amd.plan import BatchLaunch
+    from oracle.step import ReferenceMonarchMuon
+    from test_gpu_parity import BF16_TOL, blocks_rel
+    gen = torch.Generator().manual_seed(41)
+    spec = [((2, 256, 256), torch.bfloat16), ((1, 256, 256), torch.float32), ((1, 256, 256), torch.bfloat16),
+            ((2, 688, 256), torch.float32), ((1, 688, 256), torch.bfloat16)]
+    draws = [(torch.randn(s, generator=gen) * 0.02, torch.randn(s, generator=gen) * 1e-3,
+              torch.randn(s, generator=gen) * 1e-3, dt) for s, dt in spec]
+
+    def build(device, cls, **kw):
+        ps = []
+        for w, g, _, dt in draws:
+            p = w.to(dt).to(device).requires_grad_(True)
+            p.grad = g.to(dt).to(device)
+            ps.append(p)
+        opt = cls(ps, [], lr=0.02, momentum=0.95, **kw)
+        for p, (_, _, b, _) in zip(ps, draws):
+            opt.state[p]["momentum_buffer"] = b.to(device)   # fp32 buffers for every parameter
+        return ps, opt
+
+    gp, gopt = build(DEV, MonarchMuonOptimizer)
+    cp, copt = build("cpu", ReferenceMonarchMuon, variant="membench")
+    for _ in range(2):
+        gopt.step()
+        copt.step()
+    torch.cuda.synchronize()
+    groups = gopt._muon_planner.groups
+    assert [(g.rows, g.cols, g.nblocks, g.struct.param_dtype) for g in groups] == \
+        [(256, 256, 3, 1), (256, 256, 1, 0), (688, 256, 2, 0), (688, 256, 1, 1)]
+    batches = [u for u in gopt._muon_planner.units if isinstance(u, BatchLaunch)]
+    assert [[(g.rows, g.nblocks) for g in b.members] for b in batches] == [[(256, 3), (256, 1)], [(688, 2), (688, 1)]]
+    for p, q in zip(gp, cp):
+        assert p.dtype == q.dtype
+        assert blocks_rel(p, q).max() <= BF16_TOL
+        assert torch.equal(gopt.state[p]["momentum_buffer"].cpu(), copt.state[q]["momentum_buffer"])

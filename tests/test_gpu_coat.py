@@ -57,10 +57,16 @@ def _sync(gparams, gopt, cparams, copt):
             copt.state[q] = {k: (v.clone() if torch.is_tensor(v) else v) for k, v in gopt.state[p].items()}
 
 
-def _compare_codes(st, name, value, signed, blocks=None, stats=None):
-    """GPU state ``st[name]`` (codes + metadata) against ``codec.quantize(value)``.
-    ``blocks``: indices of the leading-dimension slices to compare (each a whole
-    number of 128-groups), or None for all."""
+FMT = {torch.float8_e4m3fn: ("E4M3", 448.0, 2.0 ** -4, 2.0 ** -10),
+       torch.float8_e5m2: ("E5M2", 57344.0, 2.0 ** -3, 2.0 ** -17)}   # name, max, relative and subnormal rounding
+
+
+def _compare_codes(st, name, value, signed, blocks=None, stats=None, expand_min=16):
+    """GPU state ``st[name]`` (codes + metadata, in the state's FP8 format)
+    against ``codec.quantize(value)``.  ``blocks``: indices of the
+    leading-dimension slices to compare (each a whole number of 128-groups), or
+    None for all."""
+    fmt, fmax, rel_q, abs_q = FMT[st[name].dtype]
     codes = st[name].view(torch.uint8)
     meta = [st[f"{k}_{name}"] for k in ("scale", "expand", "sqrt_minmax")]
     value = value.detach().float()
@@ -71,17 +77,17 @@ def _compare_codes(st, name, value, signed, blocks=None, stats=None):
         meta = [torch.cat([m[b * gpb:(b + 1) * gpb] for b in blocks]) for m in meta]
         value = torch.cat([value[b].reshape(-1) for b in blocks])
     x = value.cpu().numpy().reshape(-1)
-    ref = codec.quantize(x, signed)
+    ref = codec.quantize(x, signed, fmt, expand_min)
     ours = codes.cpu().numpy().reshape(-1)
     sc, ex, smm = (m.cpu().numpy() for m in meta)
     diff = np.abs(ours.astype(np.int32) - ref[0].astype(np.int32))
     ok = ex == ref[2]                              # groups whose expansion agrees
     okel = np.repeat(ok, 128)[:x.size]
-    # the decoder sees the metadata only through absmax = smm (448 scale)^(1/expand)
-    # (decode(c) = (c scale)^(1/expand) smm = (c/448)^(1/expand) absmax)
+    # the decoder sees the metadata only through absmax = smm (fmax scale)^(1/expand)
+    # (decode(c) = (c scale)^(1/expand) smm = (c/fmax)^(1/expand) absmax)
     e64 = ex.astype(np.float64)
-    amax_ours = smm.astype(np.float64) * (448.0 * sc.astype(np.float64)) ** (1.0 / e64)
-    amax_ref = ref[3].astype(np.float64) * (448.0 * ref[1].astype(np.float64)) ** (1.0 / ref[2].astype(np.float64))
+    amax_ours = smm.astype(np.float64) * (fmax * sc.astype(np.float64)) ** (1.0 / e64)
+    amax_ref = ref[3].astype(np.float64) * (fmax * ref[1].astype(np.float64)) ** (1.0 / ref[2].astype(np.float64))
     out = dict(max_code_diff=int(diff[okel].max(initial=0)),
                code_mismatch=float(np.mean(diff[okel] != 0)) if okel.any() else 0.0,
                expand_mismatch=float(np.mean(~ok)) if ok.size else 0.0,
@@ -94,16 +100,17 @@ def _compare_codes(st, name, value, signed, blocks=None, stats=None):
     assert out["expand_mismatch"] <= 1e-3, (name, out)
     assert out["absmax_rel"] <= 1e-5, (name, out)
     # every element: our codes decode (with our metadata) to the value within
-    # the e4m3 round-trip bound (q = 448 (|x|/absmax)^expand is kept to 2^-4
-    # relative, 2^-10 absolute when subnormal; the decoder raises to 1/expand)
-    dec = codec.dequantize(ours, sc, ex, smm, signed).astype(np.float64)
+    # the format's round-trip bound (q = fmax (|x|/absmax)^expand is kept to
+    # 2^-4 relative (e4m3; e5m2 2^-3), 2^-10 (2^-17) absolute when subnormal;
+    # the decoder raises to 1/expand)
+    dec = codec.dequantize(ours, sc, ex, smm, signed, fmt).astype(np.float64)
     xd = x.astype(np.float64)
     grp = np.arange(x.size) // 128
     amax = np.zeros(ok.size)
     np.maximum.at(amax, grp, np.abs(xd))
     e = ex[grp].astype(np.float64)
-    q = 448.0 * (np.abs(xd) / np.maximum(amax[grp], 1e-300)) ** e
-    eq = np.maximum(2.0 ** -4, 2.0 ** -10 / np.maximum(q, 1e-300))
+    q = fmax * (np.abs(xd) / np.maximum(amax[grp], 1e-300)) ** e
+    eq = np.maximum(rel_q, abs_q / np.maximum(q, 1e-300))
     bound = np.maximum(1 - np.clip(1 - eq, 0, None) ** (1.0 / e), (1 + eq) ** (1.0 / e) - 1) + 1e-5
     nz = xd != 0
     # plus an absolute 4e-6 of the group maximum: the two implementations'
@@ -224,3 +231,81 @@ def test_membench_fp8_states_6p89b_layer_against_oracle():
                 _compare_codes(gopt.state[p], sname, copt.state[q][sname], signed, stats=stats)
         mc = max(s["code_mismatch"] for _, s in stats)
         print(f"6.89b-nb4-fp8 layer step {step + 1}: worst weight error {worst:.3e}, worst code-mismatch {mc:.2e}")
+
+
+@pytest.mark.parametrize("first,second,emin", [("E5M2", "E5M2", 16), ("E4M3", "E5M2", 8), ("E5M2", "E4M3", 32)])
+def test_fp8_state_formats_and_expand_min_against_oracle(first, second, emin):
+    """The formats and expand_min COAT's config exposes
+    (``_fp8_quantization_config.py:23-26``): first_order_bit for the momentum and
+    exp_avg, second_order_bit for exp_avg_sq (``coat_state_muon.py:121-123``),
+    on the toy configuration (pretrain copy, fp32) for three steps."""
+    w, draws = _workload_params("toy", None, 256)
+    gm, ga = _params(draws, torch.float32)
+    cm, ca = _params(draws, torch.float32)
+    qa = QuantizationConfig(first_order_bit=first, second_order_bit=second, expand_min=emin)
+    gopt = CoatStateMonarchMuon(gm, ga, lr=0.02, momentum=0.95, qargs=qa, ns_dtype=None)
+    copt = ReferenceCoatStateMonarchMuon(cm, ca, lr=0.02, momentum=0.95, variant="pretrain")
+    f8 = {"E4M3": torch.float8_e4m3fn, "E5M2": torch.float8_e5m2}
+    copt.dtypes = {"momentum_buffer": f8[first], "exp_avg": f8[first], "exp_avg_sq": f8[second]}
+    copt.expand_min = emin
+    copt.keep_values = True
+    for step in range(3):
+        if step:
+            _sync(gm + ga, gopt, cm + ca, copt)
+        copt.step()
+        gopt.step()
+        torch.cuda.synchronize()
+        stats = []
+        for p, q in zip(gm + ga, cm + ca):
+            assert blocks_rel(p, q).max().item() <= F32_TOL, step
+            for sname, signed in FP8_STATES.items():
+                if sname in copt.values.get(q, {}):
+                    assert gopt.state[p][sname].dtype == copt.dtypes[sname]
+                    _compare_codes(gopt.state[p], sname, copt.values[q][sname], signed, stats=stats, expand_min=emin)
+                    assert np.all(gopt.state[p][f"expand_{sname}"].cpu().numpy() * emin % 1 == 0)
+        print(f"{first}/{second} expand_min {emin} step {step + 1}: worst code-mismatch "
+              f"{max(s['code_mismatch'] for _, s in stats):.2e}")
+
+
+@pytest.mark.parametrize("variant,dtype", [("pretrain", torch.float32), ("membench", torch.bfloat16)])
+def test_fp8_states_with_groups_straddling_blocks_against_oracle(variant, dtype):
+    """Monarch factors whose blocks hold a number of elements that is not a
+    multiple of 128 (a 129-column tensor as in ``test_coat_state_muon.py:27``):
+    the reference quantizes each state as one flat tensor, so groups straddle
+    blocks and the last one is short (``coat_state_muon.py:27-28,53-58``).
+    Three steps against the oracle, beside factors whose blocks do align."""
+    g = torch.Generator().manual_seed(33)
+    shapes = [((2, 129, 100), True), ((3, 100, 129), True), ((2, 64, 64), True), ((1, 40, 33), True),
+              ((2, 129, 100), True), ((1000, 129), False), ((77,), False)]
+    draws = [(None, m, torch.randn(s, generator=g) * 0.02, torch.randn(s, generator=g) * 1e-3, None)
+             for s, m in shapes]
+    gm, ga = _params(draws, dtype)
+    cm, ca = _params(draws, dtype)
+    ns = None if variant == "pretrain" else torch.bfloat16
+    gopt = CoatStateMonarchMuon(gm, ga, lr=0.02, momentum=0.95, qargs=QuantizationConfig(), ns_dtype=ns)
+    copt = ReferenceCoatStateMonarchMuon(cm, ca, lr=0.02, momentum=0.95, variant=variant)
+    copt.keep_values = True
+    tol = _weights_bar(dtype, ns)
+    gen = torch.Generator().manual_seed(34)
+    for step in range(3):
+        if step:
+            for p, q in zip(gm + ga, cm + ca):   # new gradients each step
+                nxt = (torch.randn(p.shape, generator=gen) * 1e-3).to(dtype)
+                p.grad = nxt.to(DEV)
+                q.grad = nxt.to(DEV)
+            _sync(gm + ga, gopt, cm + ca, copt)
+        copt.step()
+        gopt.step()
+        torch.cuda.synchronize()
+        stats = []
+        for p, q in zip(gm + ga, cm + ca):
+            e = blocks_rel(p, q).max().item()
+            assert e <= tol, (step, tuple(p.shape), e)
+            for sname, signed in FP8_STATES.items():
+                if sname in copt.values.get(q, {}):
+                    st = gopt.state[p]
+                    assert st[sname].dtype == torch.float8_e4m3fn and st[sname].shape == p.shape
+                    assert st[f"scale_{sname}"].numel() == (p.numel() + 127) // 128
+                    _compare_codes(st, sname, copt.values[q][sname], signed, stats=stats)
+        print(f"{variant} straddling groups step {step + 1}: worst code-mismatch "
+              f"{max(s['code_mismatch'] for _, s in stats):.2e}")

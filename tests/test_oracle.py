@@ -170,17 +170,31 @@ def test_shape_rule_matches_reference_parameter_counts(layers, embd, inter, expe
 
 
 # ---------------------------------------------------------------- FP8 codec
-def test_e4m3_encoder_matches_torch_cast():
-    x = np.concatenate([np.linspace(-460, 460, 20001, dtype=np.float32),
-                        np.float32(2.0) ** np.arange(-12, 9, 0.125, dtype=np.float32),
-                        -np.float32(2.0) ** np.arange(-12, 9, 0.125, dtype=np.float32),
-                        np.array([0.0, -0.0, 2 ** -10, 3 * 2 ** -11], dtype=np.float32)])
-    clipped = np.clip(x, -448, 448)
-    ours = codec.e4m3_encode(x)
-    ref = torch.from_numpy(clipped).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+FMTS = {"E4M3": (torch.float8_e4m3fn, 448.0, 0x7E), "E5M2": (torch.float8_e5m2, 57344.0, 0x7B)}
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+def test_fp8_encoder_matches_torch_cast(fmt):
+    dt, fmax, _ = FMTS[fmt]
+    lo = -12 if fmt == "E4M3" else -19
+    hi = 9 if fmt == "E4M3" else 16
+    x = np.concatenate([np.linspace(-1.03 * fmax, 1.03 * fmax, 20001, dtype=np.float32),
+                        np.float32(2.0) ** np.arange(lo, hi, 0.125, dtype=np.float32),
+                        -np.float32(2.0) ** np.arange(lo, hi, 0.125, dtype=np.float32),
+                        np.array([0.0, -0.0], dtype=np.float32)])
+    # every representable value and every midpoint between neighbours (ties to even)
+    allv = np.unique(np.abs(torch.arange(256, dtype=torch.uint8).view(dt).float().numpy()))
+    allv = allv[np.isfinite(allv)]
+    mids = ((allv[1:].astype(np.float64) + allv[:-1]) / 2).astype(np.float32)
+    x = np.concatenate([x, allv, -allv, mids, -mids])
+    clipped = np.clip(x, -fmax, fmax)
+    ours = codec.fp8_encode(x, fmt)
+    ref = torch.from_numpy(clipped).to(dt).view(torch.uint8).numpy()
     np.testing.assert_array_equal(ours, ref)
-    np.testing.assert_array_equal(codec.e4m3_decode(ours),
-                                  torch.from_numpy(ref).view(torch.float8_e4m3fn).float().numpy())
+    np.testing.assert_array_equal(codec.fp8_decode(ours, fmt), torch.from_numpy(ref).view(dt).float().numpy())
+    codes = np.arange(256, dtype=np.uint8)
+    np.testing.assert_array_equal(codec.fp8_decode(codes, fmt),
+                                  torch.from_numpy(codes).view(dt).float().numpy())
 
 
 def _decades(n, seed):
@@ -188,22 +202,26 @@ def _decades(n, seed):
     return (rng.standard_normal(n) * np.logspace(-6, 1, n)).astype(np.float32)
 
 
+@pytest.mark.parametrize("fmt", list(FMTS))
 @pytest.mark.parametrize("signed", [True, False])
-def test_codec_round_trip_bound(signed):
+def test_codec_round_trip_bound(signed, fmt):
     x = _decades(1000 * 129, 9).reshape(1000, 129)      # tail group + 7 decades (test_coat_state_muon.py:27-28)
     if not signed:
         x = x * x
-    q, sc, ex, smm = codec.quantize(x, signed)
-    y = codec.dequantize(q, sc, ex, smm, signed).reshape(x.shape)
-    # The encoder stores q = 448 (|x|/absmax)^expand; e4m3 keeps q to a relative
-    # 2^-4 when normal (q >= 2^-6) and to an absolute 2^-10 when subnormal.  The
-    # decoder raises back to 1/expand, so |y/x - 1| <= 1 - (1 - eq)^(1/expand).
+    fmax = FMTS[fmt][1]
+    q, sc, ex, smm = codec.quantize(x, signed, fmt)
+    y = codec.dequantize(q, sc, ex, smm, signed, fmt).reshape(x.shape)
+    # The encoder stores q = fmax (|x|/absmax)^expand; the format keeps q to a
+    # relative 2^-(mbits+1) when normal and to an absolute half of its smallest
+    # subnormal below.  The decoder raises back to 1/expand, so
+    # |y/x - 1| <= 1 - (1 - eq)^(1/expand).
+    rel_q, abs_q = (2.0 ** -4, 2.0 ** -10) if fmt == "E4M3" else (2.0 ** -3, 2.0 ** -17)
     xf, yf = x.reshape(-1).astype(np.float64), y.reshape(-1).astype(np.float64)
     groups = np.arange(xf.size) // 128
     amax = np.maximum.reduceat(np.abs(xf), np.arange(0, xf.size, 128))[groups]
     e = ex[groups].astype(np.float64)
-    q = 448.0 * (np.abs(xf) / amax) ** e
-    eq = np.maximum(2.0 ** -4, 2.0 ** -10 / np.maximum(q, 1e-300))
+    qv = fmax * (np.abs(xf) / amax) ** e
+    eq = np.maximum(rel_q, abs_q / np.maximum(qv, 1e-300))
     bound = np.maximum(1 - np.clip(1 - eq, 0, None) ** (1.0 / e), (1 + eq) ** (1.0 / e) - 1) + 1e-5
     rel = np.abs(yf - xf) / np.maximum(np.abs(xf), 1e-300)
     nz = xf != 0
@@ -212,58 +230,87 @@ def test_codec_round_trip_bound(signed):
     assert np.all(np.sign(y.reshape(-1)) == np.sign(x.reshape(-1)) * (y.reshape(-1) != 0)) or not signed
 
 
-def test_codec_special_groups():
+@pytest.mark.parametrize("fmt", list(FMTS))
+def test_codec_special_groups(fmt):
+    fmax = FMTS[fmt][1]
     const = np.full(128, 0.37, dtype=np.float32)
-    q, sc, ex, smm = codec.quantize(const, True)
+    q, sc, ex, smm = codec.quantize(const, True, fmt)
     assert ex[0] == 1.0                                    # ratio 1 -> expand = 1
-    np.testing.assert_allclose(codec.dequantize(q, sc, ex, smm, True), const, rtol=2 ** -4)
+    np.testing.assert_allclose(codec.dequantize(q, sc, ex, smm, True, fmt), const, rtol=2 ** -3)
     z = np.zeros(300, dtype=np.float32)
-    q, sc, ex, smm = codec.quantize(z, True)
-    assert np.all(q == 0) and np.all(codec.dequantize(q, sc, ex, smm, True) == 0)
-    # group of 2 decades: expand = floor(log2(448^2/2)/log2(100)*16)/16
+    q, sc, ex, smm = codec.quantize(z, True, fmt)
+    assert np.all(q == 0) and np.all(codec.dequantize(q, sc, ex, smm, True, fmt) == 0)
+    # group of 2 decades: expand = floor(log2(fmax^2/2)/log2(100)*16)/16
     x = np.array([1.0, 100.0] * 64, dtype=np.float32)
-    _, _, ex, smm = codec.quantize(x, False)
-    assert ex[0] == np.floor(np.log2(np.float32(100352.0)) / np.log2(np.float32(100.0)) * 16) / 16
+    _, _, ex, smm = codec.quantize(x, False, fmt)
+    upper = np.float32(fmax) * np.float32(fmax) / np.float32(2)
+    assert ex[0] == np.floor(np.log2(upper) / np.log2(np.float32(100.0)) * 16) / 16
     assert smm[0] == np.float32(10.0)
+    # both signed zeros store +0's code (the masked 0.0 of coat_state_muon.py:79)
+    v = np.array([1.0, -0.0, 0.0, -0.25] + [0.5] * 124, dtype=np.float32)
+    q, *_ = codec.quantize(v, True, fmt)
+    assert q[1] == 0 and q[2] == 0 and q[3] >> 7 == 1
 
 
-def test_codec_group_max_encodes_to_fp8_max():
-    # q = sign * (|x|/smm)^e / ((absmax/smm)^e / 448): the largest |value| of every
-    # group lands on +-448 (code 0x7E), which pins scale against expand and smm
+@pytest.mark.parametrize("emin", [16, 8, 4, 1, 32])
+def test_codec_expand_min(emin):
+    # expand = floor(log2(448^2/2) / log2(ratio) * emin) / emin, at least 1/emin
+    # (coat_state_muon.py:69-71 with the config's expand_min)
+    upper = np.float32(448.0) * np.float32(448.0) / np.float32(2)
+    for ratio in (100.0, 1e4, 3.0, 1e30):
+        x = np.array([1.0, ratio] * 64, dtype=np.float32)
+        _, _, ex, _ = codec.quantize(x, True, "E4M3", emin)
+        r = np.float32(ratio)
+        raw = np.float32(np.floor(np.float32(np.log2(upper) / np.log2(r)) * np.float32(emin)) / np.float32(emin))
+        assert ex[0] == max(raw, np.float32(1.0) / np.float32(emin)), (emin, ratio, ex[0])
+        assert ex[0] * emin == np.floor(ex[0] * emin)                     # a multiple of 1/emin
+    # the floor at 1/emin acts for a group spanning more than 16.6 * emin octaves
+    x = np.array([1e-30, 1e30] * 64, dtype=np.float32)
+    assert codec.quantize(x, True, "E4M3", 1)[2][0] == 1.0
+
+
+@pytest.mark.parametrize("fmt", list(FMTS))
+def test_codec_group_max_encodes_to_fp8_max(fmt):
+    # q = sign * (|x|/smm)^e / ((absmax/smm)^e / fmax): the largest |value| of every
+    # group lands on +-fmax, which pins scale against expand and smm
+    _, fmax, maxcode = FMTS[fmt]
     x = _decades(1000 * 129, 10)
     for signed in (True, False):
         v = x if signed else x * x
-        q, sc, ex, smm = codec.quantize(v, signed)
+        q, sc, ex, smm = codec.quantize(v, signed, fmt)
         g = (v.size + 127) // 128
         pad = np.zeros(g * 128, dtype=np.float32)
         pad[:v.size] = v
         top = np.argmax(np.abs(pad.reshape(g, 128)), axis=1) + np.arange(g) * 128
-        assert np.all(q[top] & 0x7F == 0x7E)
+        assert np.all(q[top] & 0x7F == maxcode)
         assert np.all((q[top] >> 7) == (pad[top] < 0))
-        # and it decodes back to that value within e4m3 + power rounding
-        d = codec.dequantize(q, sc, ex, smm, signed)
+        # and it decodes back to that value within the format + power rounding
+        d = codec.dequantize(q, sc, ex, smm, signed, fmt)
         np.testing.assert_allclose(d[top], pad[top], rtol=1e-5)
 
 
-def test_codec_power_of_four_homogeneity():
+@pytest.mark.parametrize("fmt", list(FMTS))
+def test_codec_power_of_four_homogeneity(fmt):
     # scaling a group by 4 (or 1/4) scales absmax, absmin and sqrt(absmax)*sqrt(absmin)
     # exactly (sqrt(4a) = 2 sqrt(a) in IEEE arithmetic), so codes, scale and expand
     # are unchanged and sqrt_minmax is scaled by exactly 4; the decoder is linear in it
     x = _decades(1000 * 129, 11)
     for signed in (True, False):
         v = x if signed else x * x
-        q, sc, ex, smm = codec.quantize(v, signed)
+        q, sc, ex, smm = codec.quantize(v, signed, fmt)
         for f in (np.float32(4.0), np.float32(0.25)):
-            q2, sc2, ex2, smm2 = codec.quantize(v * f, signed)
+            q2, sc2, ex2, smm2 = codec.quantize(v * f, signed, fmt)
             np.testing.assert_array_equal(q2, q)
             np.testing.assert_array_equal(sc2, sc)
             np.testing.assert_array_equal(ex2, ex)
             np.testing.assert_array_equal(smm2, smm * f)
-        d = codec.dequantize(q, sc, ex, smm, signed)
-        np.testing.assert_array_equal(codec.dequantize(q, sc, ex, smm * np.float32(4), signed), d * np.float32(4))
+        d = codec.dequantize(q, sc, ex, smm, signed, fmt)
+        np.testing.assert_array_equal(codec.dequantize(q, sc, ex, smm * np.float32(4), signed, fmt),
+                                      d * np.float32(4))
 
 
-def test_codec_halving_after_dequantize():
+@pytest.mark.parametrize("fmt", list(FMTS))
+def test_codec_halving_after_dequantize(fmt):
     # the pattern of test_coat_state_muon.py:40-51 (dequantize, halve exactly,
     # requantize): the halved group keeps its codes and expansion, and its
     # sqrt_minmax and scale move by at most an ulp or two (sqrt(a/2) is not
@@ -271,15 +318,15 @@ def test_codec_halving_after_dequantize():
     x = _decades(1000 * 129, 12)
     for signed in (True, False):
         v = x if signed else x * x
-        d = codec.dequantize(*codec.quantize(v, signed), signed)
-        full = codec.quantize(d, signed)
-        half = codec.quantize(d * np.float32(0.5), signed)
+        d = codec.dequantize(*codec.quantize(v, signed, fmt), signed, fmt)
+        full = codec.quantize(d, signed, fmt)
+        half = codec.quantize(d * np.float32(0.5), signed, fmt)
         np.testing.assert_array_equal(half[0], full[0])
         np.testing.assert_array_equal(half[2], full[2])
         np.testing.assert_allclose(half[3], full[3] * np.float32(0.5), rtol=3e-7, atol=0)
-        # scale = (absmax/smm)^expand / 448: an ulp of smm plus the division's
+        # scale = (absmax/smm)^expand / fmax: an ulp of smm plus the division's
         # rounding move the base by up to ~1.5 ulps, which the power multiplies
-        # by expand; pow and the division by 448 add an ulp each
+        # by expand; pow and the division by fmax add an ulp each
         rel = np.abs(half[1].astype(np.float64) / full[1] - 1)
         assert np.all(rel <= (2 * full[2].astype(np.float64) + 3) * 2.0 ** -23)
 
