@@ -184,9 +184,11 @@ def stage_exec_flops(kind, gl):
     32x32 MFMA tiles on or above the diagonal)."""
     lay = gl.ws.layout
     N, mp, np_ = gl.nblocks, lay.mp, lay.np_
-    if gl.struct.ns_dtype == 0:   # fp32 kernels: every tile of the padded products
+    if gl.struct.ns_dtype == 0:   # fp32 kernels: 128 x 128 tiles, SYRK / POLY the upper ones only
         kx = -(-lay.n // 32) * 32   # SYRK's K: n rounded up to the 32-deep K tiles
-        full = {"syrk": mp * mp * kx, "poly": mp ** 3, "px": mp * mp * np_, "px_apply": mp * mp * np_}
+        nt = mp // 128
+        up = (nt * (nt + 1) / 2) / (nt * nt)
+        full = {"syrk": mp * mp * kx * up, "poly": mp ** 3 * up, "px": mp * mp * np_, "px_apply": mp * mp * np_}
         return 2.0 * full.get(kind, 0) * N
     nt = mp // 256
     sym = (nt * (nt - 1) / 2 + nt * 36 / 64) / (nt * nt)
@@ -700,9 +702,11 @@ def stage_bytes(kind, gl):
     parameter block read and written instead of X'."""
     lay = gl.ws.layout
     N, mp, np_ = gl.nblocks, lay.mp, lay.np_
-    if gl.struct.ns_dtype == 0:   # fp32 kernels: every tile of the padded products
+    if gl.struct.ns_dtype == 0:   # fp32 kernels: 128 x 128 tiles, SYRK / POLY the upper ones only
         kx = -(-lay.n // 32) * 32   # SYRK's K: n rounded up to the 32-deep K tiles
-        full = {"syrk": mp * mp * kx, "poly": mp ** 3, "px": mp * mp * np_, "px_apply": mp * mp * np_}
+        nt = mp // 128
+        up = (nt * (nt + 1) / 2) / (nt * nt)
+        full = {"syrk": mp * mp * kx * up, "poly": mp ** 3 * up, "px": mp * mp * np_, "px_apply": mp * mp * np_}
         return 2.0 * full.get(kind, 0) * N
     nt = mp // 256
     up = nt * (nt + 1) // 2 * 256 * 256 * 2

@@ -48,8 +48,8 @@ constexpr uint32_t OOB = 0x80000000u;
 __device__ __forceinline__ i32x4 buffer_rsrc(const char* base) {
   const uint64_t a = reinterpret_cast<uint64_t>(base);
   i32x4 r;
-  r[0] = __builtin_amdgcn_readfirstlane(int(uint32_t(a)));
-  r[1] = __builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32) & 0xffffu));
+  r[0] = __builtin_amdgcn_readfirstlane(int(low_word(a)));
+  r[1] = __builtin_amdgcn_readfirstlane(int(high_word(a) & 0xffffu));
   r[2] = int(OOB);
   r[3] = 0x00020000;
   return r;

@@ -5,8 +5,19 @@
 #include <stdint.h>
 
 #include "../../include/mmuon.h"
+#include "addr.hpp"
 
 namespace mmuon {
+
+// p made wave-uniform: both address words read from the first active lane
+// and joined as unsigned words (join_words).
+template <class T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(low_word(a))));
+  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(high_word(a))));
+  return reinterpret_cast<T*>(join_words(lo, hi));
+}
 
 // ---------------------------------------------------------------------------
 // bf16 <-> fp32.  bf16 is carried as its raw 16-bit pattern; conversion is

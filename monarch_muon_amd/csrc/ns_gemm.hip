@@ -792,127 +792,231 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void ns_px_bf16(NsArgs a, int total)
 
 // ---------------------------------------------------------------------------
 // fp32 Newton-Schulz (the pretrain copy keeps the buffer dtype) on the fp32
-// matrix cores (v_mfma_f32_32x32x2_f32, fp32 products and accumulation): 64x64
-// output tiles, 4 waves of 32x32, K tiles of 32 double-buffered in LDS (the
-// next tile's global loads are in flight during the current tile's MFMAs).
-// All tiles computed.
+// matrix cores (v_mfma_f32_32x32x2_f32, fp32 products and accumulation).
+// 128 x 128 output tiles per 256-thread workgroup, 4 waves of 64 x 64 (2 x 2
+// MFMA tiles of 32 x 32, 64 MFMAs per wave and K tile); K advances 32 per
+// tile, double-buffered in LDS: the next tile's global loads (into registers)
+// are in flight during the current tile's MFMAs and stored to the other buffer
+// after them.  Operands reach LDS in one of two forms:
+//   RK: operand rows, [row][k] (rows of X for SYRK; rows of A / P, and by
+//       symmetry A's columns), 33 floats per row, so the 32 lanes that read
+//       one k of 32 consecutive rows hit 32 different banks;
+//   KC: [k][col] (PX's X operand, k = rows of X), 132 floats per row, 16-B
+//       aligned for float4 stores.
+// SYRK and POLY produce symmetric matrices: only the tiles on and above the
+// diagonal are computed, each stored with its mirror (staged in LDS so both
+// stores are row-contiguous), so the stored matrix is exactly symmetric.
 // ---------------------------------------------------------------------------
-constexpr int FB = 64;
-constexpr int FK = 32;
-constexpr int FPAD = FB + 32;  // LDS row: the two half-waves of a read hit disjoint banks
+constexpr int FT = 128;                // output tile
+constexpr int FK = 32;                 // K tile
+constexpr int F_NT = 256;              // 4 waves, 2 x 2
+constexpr int RK_LD = FK + 1;
+constexpr int KC_LD = FT + 4;
+constexpr int F_OPER = FT * RK_LD;     // floats per operand buffer
+static_assert(FK * KC_LD == F_OPER, "both forms fill one operand buffer");
+constexpr int F_ST = FT + 1;           // staged tile: 129 floats per row
+static_assert(FT * F_ST <= 4 * F_OPER, "the staged tile fits in the operand buffers");
 
-// One K tile of the fp32 operands into registers: the row operand is 64 rows x
-// 32 k = 512 float4 (row idx/8, k chunk idx%8), two per thread; the column
-// operand the same from its own rows, or for PX 32 rows of X x 64 columns (row
-// idx/16, column chunk idx%16).
-struct F32Regs {
-  float4 a0, a1, b0, b1;
+// One operand's K tile in registers: 1024 float4, four per thread.
+struct F32Stage {
+  float4 v[4];
 };
 
-template <bool PX>
-__device__ __forceinline__ float4 f32_col_load(const float* rsrc, int64_t rld, const float* X, int64_t np_, int c0,
-                                               int k0, int idx) {
-  if (PX) return *reinterpret_cast<const float4*>(X + int64_t(k0 + (idx >> 4)) * np_ + c0 + 4 * (idx & 15));
-  return *reinterpret_cast<const float4*>(rsrc + int64_t(c0 + (idx >> 3)) * rld + k0 + 4 * (idx & 7));
+// rows r0 .. r0+127 of a row-major matrix (leading dimension ld), k0 .. k0+31
+__device__ __forceinline__ void f32_load_rows(F32Stage& g, const float* src, int64_t ld, int r0, int k0) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = threadIdx.x + F_NT * j;
+    g.v[j] = *reinterpret_cast<const float4*>(src + int64_t(r0 + (idx >> 3)) * ld + k0 + 4 * (idx & 7));
+  }
+}
+__device__ __forceinline__ void f32_store_rk(const F32Stage& g, float* s) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = threadIdx.x + F_NT * j;
+    float* d = s + (idx >> 3) * RK_LD + 4 * (idx & 7);
+    d[0] = g.v[j].x;
+    d[1] = g.v[j].y;
+    d[2] = g.v[j].z;
+    d[3] = g.v[j].w;
+  }
+}
+// rows k0 .. k0+31 of X (leading dimension ld), columns c0 .. c0+127
+__device__ __forceinline__ void f32_load_kc(F32Stage& g, const float* X, int64_t ld, int c0, int k0) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = threadIdx.x + F_NT * j;
+    g.v[j] = *reinterpret_cast<const float4*>(X + int64_t(k0 + (idx >> 5)) * ld + c0 + 4 * (idx & 31));
+  }
+}
+__device__ __forceinline__ void f32_store_kc(const F32Stage& g, float* s) {
+  // a native 4-wide vector store (a float4 struct copy here kept the staged
+  // tile in scratch memory)
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = threadIdx.x + F_NT * j;
+    const f32x4_t v = {g.v[j].x, g.v[j].y, g.v[j].z, g.v[j].w};
+    *reinterpret_cast<f32x4_t*>(s + (idx >> 5) * KC_LD + 4 * (idx & 31)) = v;
+  }
 }
 
-template <bool PX>
-__device__ __forceinline__ void f32_load(F32Regs& g, const float* rsrc, int64_t rld, const float* X, int64_t np_,
-                                         int r0, int c0, int k0) {
-  const int i0 = threadIdx.x, i1 = threadIdx.x + 256;
-  g.a0 = *reinterpret_cast<const float4*>(rsrc + int64_t(r0 + (i0 >> 3)) * rld + k0 + 4 * (i0 & 7));
-  g.a1 = *reinterpret_cast<const float4*>(rsrc + int64_t(r0 + (i1 >> 3)) * rld + k0 + 4 * (i1 & 7));
-  g.b0 = f32_col_load<PX>(rsrc, rld, X, np_, c0, k0, i0);
-  g.b1 = f32_col_load<PX>(rsrc, rld, X, np_, c0, k0, i1);
+// Upper tile t of an nt x nt grid of tiles (ti <= tj), row-major over the
+// upper triangle.
+__device__ __forceinline__ void f32_sym_tile(int t, int nt, int& ti, int& tj) {
+  int i = 0;
+  while (t >= nt - i) {
+    t -= nt - i;
+    ++i;
+  }
+  ti = i;
+  tj = i + t;
 }
 
-template <int PAD>
-__device__ __forceinline__ void f32_store_t(const float4& v, float (*s)[PAD], int idx) {
-  const int r = idx >> 3, kc = 4 * (idx & 7);
-  s[kc][r] = v.x;
-  s[kc + 1][r] = v.y;
-  s[kc + 2][r] = v.z;
-  s[kc + 3][r] = v.w;
-}
-
-// The registers of f32_load into LDS buffers [k][row] / [k][col].
-template <bool PX, int PAD>
-__device__ __forceinline__ void f32_store(const F32Regs& g, float (*sa)[PAD], float (*sb)[PAD]) {
-  const int i0 = threadIdx.x, i1 = threadIdx.x + 256;
-  f32_store_t<PAD>(g.a0, sa, i0);
-  f32_store_t<PAD>(g.a1, sa, i1);
-  if (PX) {
-    *reinterpret_cast<float4*>(&sb[i0 >> 4][4 * (i0 & 15)]) = g.b0;
-    *reinterpret_cast<float4*>(&sb[i1 >> 4][4 * (i1 & 15)]) = g.b1;
-  } else {
-    f32_store_t<PAD>(g.b0, sb, i0);
-    f32_store_t<PAD>(g.b1, sb, i1);
+// Add v to the diagonal entries of an RK-form K tile in registers: rows rbase
+// + 0..127 of the operand, k0 .. k0+31; an element is on the diagonal when its
+// row equals its k.  The quintic's linear terms enter the products this way:
+// PX multiplies (P + a I) X, POLY A (A + (b/c) I); no epilogue reads global
+// memory and no accumulator leaves the matrix registers.
+__device__ __forceinline__ void f32_add_diag(F32Stage& g, int rbase, int k0, float v) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = threadIdx.x + F_NT * j;
+    const int d = rbase + (idx >> 3) - (k0 + 4 * (idx & 7));  // row - k of the float4's first element
+    if (d == 0) g.v[j].x += v;
+    if (d == 1) g.v[j].y += v;
+    if (d == 2) g.v[j].z += v;
+    if (d == 3) g.v[j].w += v;
   }
 }
 
 template <int STAGE, class TP>
-__global__ __launch_bounds__(256) void ns_f32(NsArgs a) {
-  __shared__ float sa[2][FK][FPAD];  // row operand, [k][row]
-  __shared__ float sb[2][FK][FPAD];  // column operand, [k][col]
-  const int b = blockIdx.z;
-  const int ti = blockIdx.y, tj = blockIdx.x;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wr = wave >> 1, wc = wave & 1;
+__global__ __launch_bounds__(F_NT) void ns_f32(NsArgs a) {
+  __shared__ __attribute__((aligned(16))) float lds[4 * F_OPER];  // [buffer 0: A, B][buffer 1: A, B]
+  constexpr bool PX = STAGE == NS_PX || STAGE == NS_PX_APPLY;
+  constexpr bool SYM = STAGE == NS_SYRK || STAGE == NS_POLY;
+  const int b = blockIdx.y;
+  int ti, tj;
+  if (SYM) {
+    f32_sym_tile(blockIdx.x, a.mp / FT, ti, tj);
+  } else {
+    const int nc = a.np / FT;
+    ti = blockIdx.x / nc;
+    tj = blockIdx.x % nc;
+  }
+  const int r0 = ti * FT, c0 = tj * FT;
   const float* X = static_cast<const float*>(a.x_in) + int64_t(b) * a.mp * a.np;
   const float* A = static_cast<const float*>(a.a_in) + int64_t(b) * a.mp * a.mp;
-  constexpr bool PX = STAGE == NS_PX || STAGE == NS_PX_APPLY;
-  const int K = STAGE == NS_SYRK ? a.kx : a.mp;
-  // row operand: 64 rows x 32 k = 512 float4 (row idx/8, k chunk idx%8), two per thread;
-  // column operand: the same from X or A rows, or for PX 32 rows of X x 64 columns
-  // (row idx/16, column chunk idx%16)
-  const float* rsrc = STAGE == NS_SYRK ? X : A;
+  const float* rsrc = STAGE == NS_SYRK ? X : A;  // rows of the row operand (and of SYRK / POLY's column operand)
   const int64_t rld = STAGE == NS_SYRK ? a.np : a.mp;
-  const int64_t np_ = a.np;
-  F32Regs g;
-  f32x16 acc = {};
+  const int K = STAGE == NS_SYRK ? a.kx : a.mp;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+  F32Stage ga, gb;
   const int KT = K / FK;
-  f32_load<PX>(g, rsrc, rld, X, np_, ti * FB, tj * FB, 0);
-  f32_store<PX, FPAD>(g, sa[0], sb[0]);
+  f32_load_rows(ga, rsrc, rld, r0, 0);
+  if (PX) f32_load_kc(gb, X, a.np, c0, 0);
+  else f32_load_rows(gb, rsrc, rld, c0, 0);
+  if (PX) f32_add_diag(ga, r0, 0, a.ca);
+  if (STAGE == NS_POLY) f32_add_diag(gb, c0, 0, a.cb / a.cc);
+  f32_store_rk(ga, lds);
+  if (PX) f32_store_kc(gb, lds + F_OPER);
+  else f32_store_rk(gb, lds + F_OPER);
   __syncthreads();
   for (int t = 0; t < KT; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < KT) f32_load<PX>(g, rsrc, rld, X, np_, ti * FB, tj * FB, (t + 1) * FK);
+    const float* sa = lds + (t & 1) * 2 * F_OPER;
+    const float* sb = sa + F_OPER;
+    if (t + 1 < KT) {
+      f32_load_rows(ga, rsrc, rld, r0, (t + 1) * FK);
+      if (PX) f32_load_kc(gb, X, a.np, c0, (t + 1) * FK);
+      else f32_load_rows(gb, rsrc, rld, c0, (t + 1) * FK);
+    }
     // 32x32x2 steps: lane l supplies row (column) l%32 at k = 2 kk + l/32
 #pragma unroll
     for (int kk = 0; kk < FK / 2; ++kk) {
-      const float av = sa[buf][2 * kk + (lane >> 5)][wr * 32 + (lane & 31)];
-      const float bv = sb[buf][2 * kk + (lane >> 5)][wc * 32 + (lane & 31)];
-      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+      const int k = 2 * kk + (lane >> 5);
+      float av[2], bv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) av[i] = sa[(wr * 64 + i * 32 + (lane & 31)) * RK_LD + k];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bv[j] = PX ? sb[k * KC_LD + wc * 64 + j * 32 + (lane & 31)] : sb[(wc * 64 + j * 32 + (lane & 31)) * RK_LD + k];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
-    if (t + 1 < KT) f32_store<PX, FPAD>(g, sa[buf ^ 1], sb[buf ^ 1]);
+    if (t + 1 < KT) {
+      float* d = lds + ((t + 1) & 1) * 2 * F_OPER;
+      if (PX) f32_add_diag(ga, r0, (t + 1) * FK, a.ca);
+      if (STAGE == NS_POLY) f32_add_diag(gb, c0, (t + 1) * FK, a.cb / a.cc);
+      f32_store_rk(ga, d);
+      if (PX) f32_store_kc(gb, d + F_OPER);
+      else f32_store_rk(gb, d + F_OPER);
+    }
     __syncthreads();
   }
-  const float s = a.scale != nullptr ? a.scale[b] : 1.f;
-  typename TP::storage* prm = nullptr;
-  if (STAGE == NS_PX_APPLY) prm = reinterpret_cast<typename TP::storage*>(a.blocks[b].param);
-  // accumulator value 4 q + e: column lane%32, row 8 q + 4 (lane/32) + e
-  const int j = tj * FB + wc * 32 + (lane & 31);
+  // stage the tile: accumulator value 4 q + e of MFMA tile (i, j) holds row
+  // 64 wr + 32 i + 8 q + 4 (lane/32) + e, column 64 wc + 32 j + lane%32
+  float* T = lds;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = ti * FB + wr * 32 + 8 * q + 4 * (lane >> 5) + e;
-      const float v = acc[4 * q + e];
-      if (STAGE == NS_SYRK) {
-        static_cast<float*>(a.out)[int64_t(b) * a.mp * a.mp + int64_t(i) * a.mp + j] = v * (s * s);
-      } else if (STAGE == NS_POLY) {
-        static_cast<float*>(a.out)[int64_t(b) * a.mp * a.mp + int64_t(i) * a.mp + j] =
-            fmaf(a.cc, v, a.cb * A[int64_t(i) * a.mp + j]);
-      } else {
-        const float u = s * fmaf(a.ca, X[int64_t(i) * a.np + j], v);
-        if (STAGE == NS_PX) {
-          static_cast<float*>(a.out)[int64_t(b) * a.mp * a.np + int64_t(i) * a.np + j] = u;
-        } else if (i < a.m && j < a.n) {
-          const int64_t o = a.transposed ? int64_t(j) * a.m + i : int64_t(i) * a.n + j;
-          TP::store(prm, o, fmaf(a.alpha, u, TP::load(prm, o)));
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = wr * 64 + i * 32 + 8 * q + 4 * (lane >> 5) + e, c = wc * 64 + j * 32 + (lane & 31);
+          T[r * F_ST + c] = acc[i][j][4 * q + e];
         }
+  __syncthreads();
+  const float s = a.scale != nullptr ? a.scale[b] : 1.f;
+  // element idx of the tile, two mappings (consecutive lanes along the
+  // destination's rows): direct (r, c) = (idx / 128, idx % 128) and mirrored
+  // (r, c) = (idx % 128, idx / 128), the latter for stores along a column of
+  // the tile (a symmetric mirror, a tall block's parameter rows)
+  if (STAGE == NS_SYRK || STAGE == NS_POLY) {
+    // SYRK: A = s^2 acc; POLY: P = c (A A + (b/c) A) = b A + c A A
+    float* out = static_cast<float*>(a.out) + int64_t(b) * a.mp * a.mp;
+    const float f = STAGE == NS_SYRK ? s * s : a.cc;
+    for (int it = 0; it < FT * FT / F_NT; ++it) {
+      const int idx = threadIdx.x + F_NT * it, r = idx >> 7, c = idx & 127;
+      // a diagonal tile takes its lower triangle from the upper one
+      const float v = (tj == ti && r > c) ? T[c * F_ST + r] : T[r * F_ST + c];
+      out[int64_t(r0 + r) * a.mp + c0 + c] = v * f;
+    }
+    if (tj != ti) {
+      for (int it = 0; it < FT * FT / F_NT; ++it) {
+        const int idx = threadIdx.x + F_NT * it, r = idx & 127, c = idx >> 7;
+        out[int64_t(c0 + c) * a.mp + r0 + r] = T[r * F_ST + c] * f;  // the mirror of (r0 + r, c0 + c)
       }
     }
+    return;
+  }
+  if (STAGE == NS_PX) {  // X' = s (a X + P X)
+    float* out = static_cast<float*>(a.out) + int64_t(b) * a.mp * a.np;
+    for (int it = 0; it < FT * FT / F_NT; ++it) {
+      const int idx = threadIdx.x + F_NT * it, r = idx >> 7, c = idx & 127;
+      out[int64_t(r0 + r) * a.np + c0 + c] = s * T[r * F_ST + c];
+    }
+    return;
+  }
+  // PX_APPLY: param += alpha X' (un-transposed); the block is (m x n) or, tall, (n x m)
+  auto* prm = reinterpret_cast<typename TP::storage*>(a.blocks[b].param);
+  for (int it = 0; it < FT * FT / F_NT; ++it) {
+    const int idx = threadIdx.x + F_NT * it;
+    const int r = a.transposed ? (idx & 127) : (idx >> 7), c = a.transposed ? (idx >> 7) : (idx & 127);
+    const int i = r0 + r, j = c0 + c;
+    if (i >= a.m || j >= a.n) continue;
+    const float u = s * T[r * F_ST + c];
+    const int64_t o = a.transposed ? int64_t(j) * a.m + i : int64_t(i) * a.n + j;
+    TP::store(prm, o, fmaf(a.alpha, u, TP::load(prm, o)));
   }
 }
 
@@ -938,15 +1042,27 @@ void launch_bf16(const NsArgs& a, hipStream_t s) {
 
 template <int STAGE, class TP>
 void launch_f32(const NsArgs& a, hipStream_t s) {
-  const int cols = (STAGE == NS_SYRK || STAGE == NS_POLY) ? a.mp : a.np;
-  const dim3 grid(cols / FB, a.mp / FB, a.N);
-  hipLaunchKernelGGL((ns_f32<STAGE, TP>), grid, dim3(256), 0, s, a);
+  const int nt = a.mp / FT;
+  const int tiles = (STAGE == NS_SYRK || STAGE == NS_POLY) ? nt * (nt + 1) / 2 : nt * (a.np / FT);
+  // blocks go to grid.y (at most 65535 per launch): larger stacks in chunks
+  const int64_t per_x = int64_t(a.mp) * a.np, per_a = int64_t(a.mp) * a.mp;
+  const int64_t per_out = (STAGE == NS_SYRK || STAGE == NS_POLY) ? per_a : per_x;
+  for (int b0 = 0; b0 < a.N; b0 += 65535) {
+    NsArgs c = a;
+    c.N = a.N - b0 < 65535 ? a.N - b0 : 65535;
+    if (a.x_in) c.x_in = static_cast<const float*>(a.x_in) + b0 * per_x;
+    if (a.a_in) c.a_in = static_cast<const float*>(a.a_in) + b0 * per_a;
+    if (a.out) c.out = static_cast<float*>(a.out) + b0 * per_out;
+    if (a.scale) c.scale = a.scale + b0;
+    if (a.blocks) c.blocks = a.blocks + b0;
+    hipLaunchKernelGGL((ns_f32<STAGE, TP>), dim3(tiles, c.N), dim3(F_NT), 0, s, c);
+  }
 }
 
 }  // namespace
 
-int ns_tile_m(int ns_dtype) { return ns_dtype == MMUON_BF16 ? BM : FB; }
-int ns_tile_n(int ns_dtype) { return ns_dtype == MMUON_BF16 ? 256 : FB; }  // pack tiles 256 columns
+int ns_tile_m(int ns_dtype) { return ns_dtype == MMUON_BF16 ? BM : FT; }
+int ns_tile_n(int ns_dtype) { return ns_dtype == MMUON_BF16 ? 256 : FT; }  // pack tiles 256 columns
 int ns_tile_k(int ns_dtype) { return ns_dtype == MMUON_BF16 ? BK : FK; }
 
 int launch_ns_stage(const NsArgs& a, int stage, int ns_dtype, int param_dtype, hipStream_t s) {
