@@ -422,11 +422,12 @@ __device__ __forceinline__ void mainloop(const uint16_t* rsrc_k, const uint16_t*
 // j = 64 wn + 32 tj + lane%32 and rows i = 128 wm + 32 ti + 8 qg + 4 (lane/32) + e,
 // (wm, wn) the wave's window.  diag: a diagonal tile of a symmetric product
 // computed by diag_plan; every computed tile above the diagonal also fills its
-// mirror below it, T[i][j] = D[i][j], and so does the upper triangle of each
-// 32 x 32 tile on the diagonal (written after, and so replacing, the values the
-// lane pairs computed below it: equal bits when both operands are one
-// symmetric matrix, rounding-level apart for SYMM's two commuting ones); its
-// diagonal entries i = j < dlim get dadd added (in fp32, before the rounding).
+// mirror below it, T[i][j] = D[i][j] (copied from the staged tile), and so does
+// the upper triangle of each 32 x 32 tile on the diagonal (written after, and
+// so replacing, the values the lane pairs computed below it: equal bits when
+// both operands are one symmetric matrix, rounding-level apart for SYMM's two
+// commuting ones); its diagonal entries i = j < dlim get dadd added (in fp32,
+// before the rounding).
 __device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI][TMJ], float f,
                                            bool diag = false, float dadd = 0.f, int dlim = 0) {
   const int tid = fresh_tid();
@@ -458,16 +459,48 @@ __device__ __forceinline__ void stage_tile(char* stage, const f32x16 (&acc)[TMI]
         const int col = wm * WM + i * 32 + qg * 8 + (lane >> 5) * 4;
         *reinterpret_cast<uint2*>(stage + tile_off(row, col)) = make_uint2(f2bf2(v[0], v[1]), f2bf2(v[2], v[3]));
       }
-      if (diag && C >= R) {
+      if (diag && C == R) {
+        // a 32 x 32 tile on the diagonal: its upper triangle replaces the
+        // values just staged below it
 #pragma unroll
         for (int qg = 0; qg < 4; ++qg)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int row = wm * WM + i * 32 + qg * 8 + (lane >> 5) * 4 + e;
             const int col = wn * WN + j * 32 + (lane & 31);
-            if (C > R || row < col)
-              *reinterpret_cast<uint16_t*>(stage + tile_off(row, col)) = f2bf(f * acc[i][j][qg * 4 + e]);
+            if (row < col) *reinterpret_cast<uint16_t*>(stage + tile_off(row, col)) = f2bf(f * acc[i][j][qg * 4 + e]);
           }
+      }
+    }
+  }
+  if (!diag) return;
+  // The mirrors of this wave's tiles above the diagonal (C > R): the tile it
+  // has just staged, T[32C + r][32R + i] = D[32R + i][32C + r], read
+  // transposed (ds_read_b64_tr_b16, as stage_cols reads) gives rows of D,
+  // stored as 16-B chunks at T[32R + i][32C + r] -- four reads and two writes
+  // per lane and tile, the staged bf16 values copied bit for bit.  The wave's
+  // LDS operations complete in order, and no other wave writes or reads
+  // either region.
+  asm volatile("" ::: "memory");
+  const int l16 = lane & 15, grp = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < TMI; ++i) {
+#pragma unroll
+    for (int j = 0; j < TMJ; ++j) {
+      const int R = wm * (WM / 32) + i, C = wn * (WN / 32) + j;
+      if (!((plan.mask >> (i * TMJ + j)) & 1) || C <= R) continue;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r0 = 32 * C + grp * 8, i0 = 32 * R + 16 * h;
+        const int tr = r0 + (l16 >> 2), tc = i0 + ((l16 & 3) << 2);
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(stage + tile_off(tr, tc)));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(stage + tile_off(tr + 4, tc)));
+        uint4 v;
+        v.x = uint32_t(uint16_t(lo[0])) | (uint32_t(uint16_t(lo[1])) << 16);
+        v.y = uint32_t(uint16_t(lo[2])) | (uint32_t(uint16_t(lo[3])) << 16);
+        v.z = uint32_t(uint16_t(hi[0])) | (uint32_t(uint16_t(hi[1])) << 16);
+        v.w = uint32_t(uint16_t(hi[2])) | (uint32_t(uint16_t(hi[3])) << 16);
+        *reinterpret_cast<uint4*>(stage + tile_off(i0 + l16, r0)) = v;
       }
     }
   }
