@@ -1092,34 +1092,56 @@ XCDS = 8  # MI355X: GRBM_GUI_ACTIVE is reported summed over the 8 XCDs' GRBMs
 
 
 def mfma_summary(args):
-    """MFMA utilisation per Newton-Schulz kernel from rocprofv3 counter runs
+    """MFMA utilisation per Newton-Schulz kernel, and the instruction mix of
+    the streaming kernels, from rocprofv3 counter runs
     (``--mfma-summary OUT.json CSV...``): executed MFMA FLOP (SQ_INSTS_MFMA x
     32768, every instruction of these kernels being v_mfma_f32_32x32x16_bf16;
     SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 where that counter was collected), the
     GFX clock the counters imply (GRBM_GUI_ACTIVE / 8 XCDs / duration) and the
     MFMA busy fraction of all 1024 SIMDs' cycles (SQ_VALU_MFMA_BUSY_CYCLES /
-    (GRBM_GUI_ACTIVE / 8 x 1024), rocprofv3's MfmaUtil)."""
+    (GRBM_GUI_ACTIVE / 8 x 1024), rocprofv3's MfmaUtil).  For the pack, AdamW
+    and FP8 kernels, where SQ_INSTS_VALU was collected: VALU, transcendental,
+    vector-memory and LDS wave instructions per dispatch and their ratios."""
     out_path, *csvs = args.mfma_summary
     s = counter_summary(csvs)
     simds = 1024
     res = {}
     for k, c in s.items():
-        if not k.startswith("ns_") or "SQ_INSTS_MFMA" not in c or "duration_ns" not in c:
+        if "duration_ns" not in c:
             continue
         secs = c["duration_ns"] * 1e-9
-        flop = c["SQ_INSTS_MFMA"] * 32768.0
-        rec = {"dispatches": c["dispatches"], "avg_ms": round(secs * 1e3, 4), "exec_flop": flop,
-               "exec_tflops": round(flop / secs / 1e12, 1),
-               "exec_frac_peak": round(flop / secs / 1e12 / PEAK_BF16_TFLOPS, 4)}
-        if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in c:
-            rec["mops_flop"] = c["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512.0
-        if "GRBM_GUI_ACTIVE" in c:
-            cycles = c["GRBM_GUI_ACTIVE"] / XCDS
-            rec["gfx_mhz"] = round(cycles / secs / 1e6, 1)
-            # what the kernel executed against the peak at the clock it ran at
-            rec["exec_frac_at_clock"] = round(flop / (cycles * simds * 1024.0), 4)
-            if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
-                rec["mfma_busy"] = round(c["SQ_VALU_MFMA_BUSY_CYCLES"] / (cycles * simds), 4)
+        rec = {"dispatches": c["dispatches"], "avg_ms": round(secs * 1e3, 4)}
+        if k.startswith("ns_") and "SQ_INSTS_MFMA" in c:
+            flop = c["SQ_INSTS_MFMA"] * 32768.0
+            rec.update({"exec_flop": flop, "exec_tflops": round(flop / secs / 1e12, 1),
+                        "exec_frac_peak": round(flop / secs / 1e12 / PEAK_BF16_TFLOPS, 4)})
+            if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in c:
+                rec["mops_flop"] = c["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512.0
+            if "GRBM_GUI_ACTIVE" in c:
+                cycles = c["GRBM_GUI_ACTIVE"] / XCDS
+                rec["gfx_mhz"] = round(cycles / secs / 1e6, 1)
+                # what the kernel executed against the peak at the clock it ran at
+                rec["exec_frac_at_clock"] = round(flop / (cycles * simds * 1024.0), 4)
+                if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+                    rec["mfma_busy"] = round(c["SQ_VALU_MFMA_BUSY_CYCLES"] / (cycles * simds), 4)
+        elif k.startswith(("ns_", "pack", "adamw", "fp8_", "block_scale", "zero_pads")) and "SQ_INSTS_VALU" in c:
+            # instruction mix (wave instructions summed over the device per dispatch)
+            for name in ("SQ_INSTS_VALU", "SQ_INSTS_VALU_TRANS_F32", "SQ_INSTS_VMEM", "SQ_INSTS_LDS", "SQ_WAVES"):
+                if name in c:
+                    rec[name] = c[name]
+            if c.get("SQ_INSTS_VMEM"):
+                rec["valu_per_vmem"] = round(c["SQ_INSTS_VALU"] / c["SQ_INSTS_VMEM"], 2)
+            if "SQ_INSTS_VALU_TRANS_F32" in c and c["SQ_INSTS_VALU"]:
+                rec["trans_frac_of_valu"] = round(c["SQ_INSTS_VALU_TRANS_F32"] / c["SQ_INSTS_VALU"], 4)
+            if "GRBM_GUI_ACTIVE" in c:
+                cycles = c["GRBM_GUI_ACTIVE"] / XCDS
+                rec["gfx_mhz"] = round(cycles / secs / 1e6, 1)
+                # VALU wave instructions per SIMD cycle (a wave64 instruction
+                # occupies its SIMD 4 cycles at full rate, 16 for a
+                # quarter-rate transcendental)
+                rec["valu_insts_per_simd_cycle"] = round(c["SQ_INSTS_VALU"] / (cycles * simds), 4)
+        else:
+            continue
         res[k] = rec
     Path(out_path).write_text(json.dumps({"simds": simds, "kernels": res}, indent=1) + "\n")
     print(json.dumps(res, indent=1))
@@ -1172,7 +1194,8 @@ def main():
                     help="summarise rocprofv3 FETCH_SIZE / WRITE_SIZE runs into OUT_JSON (HBM bytes per dispatch)")
     ap.add_argument("--mfma-summary", nargs="+", metavar=("OUT_JSON", "CSV"),
                     help="summarise rocprofv3 counter CSVs (SQ_INSTS_MFMA, SQ_VALU_MFMA_BUSY_CYCLES, "
-                         "GRBM_GUI_ACTIVE) into OUT_JSON")
+                         "GRBM_GUI_ACTIVE; or SQ_INSTS_VALU, SQ_INSTS_VALU_TRANS_F32, SQ_INSTS_VMEM, "
+                         "SQ_INSTS_LDS) into OUT_JSON")
     args = ap.parse_args()
     if args.mfma_summary:
         mfma_summary(args)

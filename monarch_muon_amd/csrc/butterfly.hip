@@ -505,15 +505,27 @@ void set_geometry(GemmArgs& a, int M, int N, int K, int G, int S) {
   a.vtiles = 8 * cdiv(int64_t(G) * a.S * a.tiles_m, 8) * a.tiles_n;
 }
 
-// Splits of a weight-gradient product (K = tokens): enough work items for one
-// per CU of a 256-CU part, at least 1024 tokens per split.  A function of the
-// shapes only, so the summation order (and the result) does not depend on the
-// device.
+// Splits of a weight-gradient product (K = tokens), at least 1024 tokens per
+// split: the S that minimises a cost model of a 256-CU part in units of one
+// token of K per tile, rounds(S) (K/S + 576) + 768 [S > 1], where a round of
+// tiles carries a fixed cost of about 576 (prologue, epilogue, store burst) and
+// the fp32 partials' reduction pass about 768.  (6.89B at 4096 tokens: the
+// 64-tile products split 4 ways, the 176-tile ones run unsplit, one round of
+// K = 4096 instead of two of 2048 plus a reduction.)  A function of the shapes
+// only, so the summation order (and the result) does not depend on the device.
 int wgrad_splits(int M, int N, int G, int64_t K) {
   const int64_t tiles = int64_t(G) * cdiv(M, BM) * cdiv(N, BN);
-  int S = 1;
-  while (tiles * S < 256 && K >= int64_t(S) * 2 * 1024) S *= 2;
-  return S;
+  int best = 1;
+  int64_t best_cost = -1;
+  for (int S = 1; S <= 64 && (S == 1 || K >= int64_t(S) * 1024); S *= 2) {
+    const int64_t rounds = (tiles * S + 255) / 256;
+    const int64_t cost = rounds * ((K + S - 1) / S + 576) + (S > 1 ? 768 : 0);
+    if (best_cost < 0 || cost < best_cost) {
+      best = S;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 template <bool AT, bool BT, bool SPLIT>
@@ -574,13 +586,20 @@ int launch_butterfly_bwd(const mmuon_butterfly_args& x, hipStream_t st) {
   void* dt = ws;
   float* part = reinterpret_cast<float*>(ws + (size_t(d.nb) * d.B * d.q * 2 + 255) / 256 * 256);
 
-  GemmArgs b1{};  // dw2[ll] = dout[:, ll]^T t[ll]  (K = tokens, split)
+  // dw2[ll] = dout[:, ll]^T t[ll]  (K = tokens, split; unsplit: bf16 straight
+  // from the tile)
+  GemmArgs b1{};
   b1.a = make_op(x.dout, int64_t(d.s) * 2, 2, int64_t(d.nb) * d.s * 2, d.s);
   b1.b = make_op(x.out1, d.B * d.q * 2, 2, int64_t(d.q) * 2, d.q);
   b1.partial = part;
+  b1.c = make_out(x.dw2, int64_t(d.s) * d.q * 2, int64_t(d.q) * 2);
   set_geometry(b1, d.s, d.q, int(d.B), d.nb, wgrad_splits(d.s, d.q, d.nb, d.B));
-  if (d.B > 0) launch_gemm_t<true, true, true>(b1, st);
-  launch_reduce(b1, make_out(x.dw2, int64_t(d.s) * d.q * 2, int64_t(d.q) * 2), st);
+  if (d.B > 0 && b1.S == 1) {
+    launch_gemm_t<true, true, false>(b1, st);
+  } else {
+    if (d.B > 0) launch_gemm_t<true, true, true>(b1, st);
+    launch_reduce(b1, b1.c, st);
+  }
   if (d.B == 0) {
     GemmArgs b4{};
     b4.partial = part;
@@ -611,9 +630,14 @@ int launch_butterfly_bwd(const mmuon_butterfly_args& x, hipStream_t st) {
   b4.a = make_op(dt, ql * 2, 2, int64_t(d.q) * 2, d.q, ql, d.B * d.q * 2);
   b4.b = make_op(x.x, int64_t(d.p) * 2, 2, n * 2, d.p);
   b4.partial = part;
+  b4.c = make_out(x.dw1, int64_t(d.q) * d.p * 2, int64_t(d.nb) * d.p * 2, ql, int64_t(d.p) * 2);
   set_geometry(b4, d.q, d.p, int(d.B), d.nb, wgrad_splits(d.q, d.p, d.nb, d.B));
-  launch_gemm_t<true, true, true>(b4, st);
-  launch_reduce(b4, make_out(x.dw1, int64_t(d.q) * d.p * 2, int64_t(d.nb) * d.p * 2, ql, int64_t(d.p) * 2), st);
+  if (b4.S == 1) {
+    launch_gemm_t<true, true, false>(b4, st);
+  } else {
+    launch_gemm_t<true, true, true>(b4, st);
+    launch_reduce(b4, b4.c, st);
+  }
   return 0;
 }
 
