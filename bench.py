@@ -1041,7 +1041,7 @@ def traffic_summary(args):
     f, wr = counter_summary([fetch_csv]), counter_summary([write_csv])
     kernels = {}
     for k in f:
-        if k in wr and (k.startswith(("ns_", "pack", "adamw", "fp8_")) or "butterfly" in k):
+        if k in wr and (k.startswith(("ns_", "pack", "adamw", "fp8_", "splitk")) or "butterfly" in k):
             b = f[k]["FETCH_SIZE"] * 1024 * fscale + wr[k]["WRITE_SIZE"] * 1024 * wscale
             kernels[k] = {"fetch_kib": f[k]["FETCH_SIZE"], "write_kib": wr[k]["WRITE_SIZE"], "bytes": b,
                           "read_bytes": f[k]["FETCH_SIZE"] * 1024 * fscale,
@@ -1095,8 +1095,9 @@ def mfma_summary(args):
     """MFMA utilisation per Newton-Schulz kernel, and the instruction mix of
     the streaming kernels, from rocprofv3 counter runs
     (``--mfma-summary OUT.json CSV...``): executed MFMA FLOP (SQ_INSTS_MFMA x
-    32768, every instruction of these kernels being v_mfma_f32_32x32x16_bf16;
-    SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 where that counter was collected), the
+    32768, every instruction of the bf16 kernels being
+    v_mfma_f32_32x32x16_bf16, x 4096 for the fp32 kernels' v_mfma_f32_32x32x2_f32;
+    SQ_INSTS_VALU_MFMA_MOPS_BF16 / _F32 x 512 where collected), the
     GFX clock the counters imply (GRBM_GUI_ACTIVE / 8 XCDs / duration) and the
     MFMA busy fraction of all 1024 SIMDs' cycles (SQ_VALU_MFMA_BUSY_CYCLES /
     (GRBM_GUI_ACTIVE / 8 x 1024), rocprofv3's MfmaUtil).  For the pack, AdamW
@@ -1112,16 +1113,23 @@ def mfma_summary(args):
         secs = c["duration_ns"] * 1e-9
         rec = {"dispatches": c["dispatches"], "avg_ms": round(secs * 1e3, 4)}
         if k.startswith("ns_") and "SQ_INSTS_MFMA" in c:
-            flop = c["SQ_INSTS_MFMA"] * 32768.0
+            # bf16 kernels: v_mfma_f32_32x32x16_bf16 (32768 FLOP, 1024 FLOP per
+            # SIMD cycle at peak); fp32 kernels: v_mfma_f32_32x32x2_f32 (4096
+            # FLOP, 64 per SIMD cycle)
+            f32 = k.startswith("ns_f32")
+            flop = c["SQ_INSTS_MFMA"] * (4096.0 if f32 else 32768.0)
+            peak = PEAK_F32_TFLOPS if f32 else PEAK_BF16_TFLOPS
             rec.update({"exec_flop": flop, "exec_tflops": round(flop / secs / 1e12, 1),
-                        "exec_frac_peak": round(flop / secs / 1e12 / PEAK_BF16_TFLOPS, 4)})
-            if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in c:
+                        "exec_frac_peak": round(flop / secs / 1e12 / peak, 4)})
+            if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in c and not f32:
                 rec["mops_flop"] = c["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512.0
+            if "SQ_INSTS_VALU_MFMA_MOPS_F32" in c and f32:
+                rec["mops_flop"] = c["SQ_INSTS_VALU_MFMA_MOPS_F32"] * 512.0
             if "GRBM_GUI_ACTIVE" in c:
                 cycles = c["GRBM_GUI_ACTIVE"] / XCDS
                 rec["gfx_mhz"] = round(cycles / secs / 1e6, 1)
                 # what the kernel executed against the peak at the clock it ran at
-                rec["exec_frac_at_clock"] = round(flop / (cycles * simds * 1024.0), 4)
+                rec["exec_frac_at_clock"] = round(flop / (cycles * simds * (64.0 if f32 else 1024.0)), 4)
                 if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
                     rec["mfma_busy"] = round(c["SQ_VALU_MFMA_BUSY_CYCLES"] / (cycles * simds), 4)
         elif k.startswith(("ns_", "pack", "adamw", "fp8_", "block_scale", "zero_pads")) and "SQ_INSTS_VALU" in c:
