@@ -202,6 +202,52 @@ def test_bf16_momentum_bit_exact_against_torch_gpu_semantics():
         assert blocks_rel(p, q).max() <= BF16_TOL
 
 
+@pytest.mark.parametrize("variant", ["membench", "pretrain"])
+def test_adamw_bf16_bit_exact_against_torch_gpu_ops(variant):
+    """The AdamW group with bf16 parameters, gradients and (optimizer-created)
+    states against the reference's op sequence executed by torch on this GPU
+    (membench monarch_muon.py:176-208 as foreach ops; pretrain :176-201 per
+    tensor): parameters, exp_avg and exp_avg_sq bit for bit over four steps
+    with new gradients before each.  Gradients span 1e-30 to 1e2 (so the second
+    moments reach bf16's subnormal range and its top), with exact zeros; the
+    shapes give ragged tails and 16-B misaligned tensors."""
+    gen = torch.Generator().manual_seed(23)
+    shapes = [(512, 300), (1000,), (77,), (33, 129), (2, 3, 5), (4096, 64)]
+    w0 = [torch.randn(s, generator=gen) * 0.02 for s in shapes]
+    grads = []
+    for _ in range(4):
+        step_g = []
+        for s in shapes:
+            mag = 10.0 ** torch.randint(-30, 3, s, generator=gen).double()
+            g = (torch.randn(s, generator=gen).double() * mag).float()
+            g[torch.rand(s, generator=gen) < 0.05] = 0.0
+            step_g.append(g)
+        grads.append(step_g)
+
+    def run(cls, **kw):
+        muon = [(torch.randn(2, 64, 64, generator=torch.Generator().manual_seed(3)) * 0.02)
+                .bfloat16().to(DEV).requires_grad_(True)]
+        adamw = [w.bfloat16().to(DEV).requires_grad_(True) for w in w0]
+        opt = cls(muon, adamw, lr=0.02, momentum=0.95, **kw)
+        for step_g in grads:
+            muon[0].grad = torch.full_like(muon[0], 1e-3)
+            for p, g in zip(adamw, step_g):
+                p.grad = g.bfloat16().to(DEV)
+            opt.step()
+        torch.cuda.synchronize()
+        return adamw, opt
+
+    ours, gopt = run(MonarchMuonOptimizer, ns_dtype=torch.bfloat16 if variant == "membench" else None)
+    ref, ropt = run(ReferenceMonarchMuon, variant=variant)
+    for p, q in zip(ours, ref):
+        assert p.dtype == q.dtype == torch.bfloat16
+        assert torch.equal(p, q), "parameters"
+        for name in ("exp_avg", "exp_avg_sq"):
+            a, b = gopt.state[p][name], ropt.state[q][name]
+            assert a.dtype == b.dtype == torch.bfloat16
+            assert torch.equal(a, b), name
+
+
 # ---------------------------------------------------------------- BASELINE configs (reduced where the CPU oracle is slow)
 def _workload_params(name, layers=None, adamw_rows=None, seed=0):
     """Seeded fp32 draws in parameter order (W, g, buf per Muon param; W, g per
