@@ -10,11 +10,9 @@ Size-independent checks over the whole step:
   into its workspace stacks, beyond 2^31 bytes -- is within 1.5x the
   reference's own bf16 error of fp64 Newton-Schulz (+2e-3), as in the
   one-layer test;
-- every block of every parameter (all 1792) equals its old value plus alpha
-  times the Newton-Schulz output the library left in its workspace, rounded
-  once to bf16 (alpha = -lr sqrt(rows/cols)): at most one bf16 step apart, and
-  bit-equal for all but a sliver of rounding ties (the expected values are
-  formed with torch ops on the GPU).
+- every block of every parameter (all 1792) equals, bit for bit, the
+  reference's apply run by torch on the GPU: a foreach add of the Newton-Schulz
+  output the library left in its workspace with alpha = -lr sqrt(rows/cols).
 """
 import ctypes as C
 
@@ -102,21 +100,18 @@ def test_full_6p89b_step():
     torch.cuda.synchronize()
     for p, r in zip(params, ref_bufs):
         assert torch.equal(opt.state[p]["momentum_buffer"], r)
-    checked, worst_frac = 0, 0.0
+    checked = 0
     for gl, stack in stacks:
-        alpha = torch.tensor(-LR * (gl.rows / gl.cols) ** 0.5, dtype=torch.float32).double()
+        alpha = -LR * (gl.rows / gl.cols) ** 0.5
         b0 = 0
         for i in gl.members:
             nb = params[i].shape[0]
-            u = stack[b0:b0 + nb]
-            expect = (w0[i].double() + alpha * u.double()).float().bfloat16()
-            got = params[i].data
-            steps = (got.view(torch.int16).int() - expect.view(torch.int16).int()).abs()
-            per_block = (steps != 0).float().mean(dim=(1, 2))
-            assert int(steps.max()) <= 1 and float(per_block.max()) < 1e-3, (i, int(steps.max()), float(per_block.max()))
-            worst_frac = max(worst_frac, float(per_block.max()))
+            expect = [w0[i].clone()]
+            # the reference's apply (membench monarch_muon.py:165-170) run by torch on the GPU
+            torch._foreach_add_(expect, [stack[b0:b0 + nb]], alpha=alpha)
+            assert torch.equal(params[i].data, expect[0]), i
             checked += nb
             b0 += nb
         assert b0 == gl.nblocks
     assert checked == 1792
-    print(f"apply checked on all {checked} blocks: worst per-block fraction of rounding-tie steps {worst_frac:.2e}")
+    print(f"apply checked on all {checked} blocks: bit-identical to torch's foreach add on the GPU")
