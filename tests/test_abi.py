@@ -130,8 +130,8 @@ def test_hbm_probe_validates_before_launching():
     """The bench-only HBM probe (bench_probe.so, apart from libmmuon.so) rejects
     every malformed request before it launches (no GPU needed); libmmuon.so
     does not export it."""
-    import bench
-    lib = bench.probe_lib()
+    import bench_studies
+    lib = bench_studies.probe_lib()
     assert not hasattr(_abi.lib(), "mmuon_hbm_stream")
     n = 1 << 20
     assert lib.probe_hbm_stream(8, 4096, 4096, n, 0, 16, None) == -1
