@@ -189,6 +189,14 @@ struct Pipe {
     static_assert(IDENT == IDENT_COL, "the column identity is the only one");
     const int l16 = lane & 15, g = lane >> 4;
     const int k16 = 16 * (g & 1) + 4 * (l16 & 3);  // first column of the lane's 8-byte chunk
+    // The read of rows rb = wm WM + 32 i + 8 q + 4 (g/2) + l16/4 sits at
+    // base + (32 i + 8 q) 64 + ((k16/8) ^ ((rb/4) % 4)) 16, and (rb/4) % 4 =
+    // (2 q + g/2) % 4 only depends on q's parity: two per-lane bases, the rest
+    // an immediate offset of the read.
+    const int rlane = wm * WM + 4 * (g >> 1) + (l16 >> 2);
+    const uint32_t base = uint32_t(rlane * 64 + (k16 & 7) * 2);
+    const uint32_t b0 = base + uint32_t(((k16 >> 3) ^ ((g >> 1) & 3)) << 4);
+    const uint32_t b1 = base + uint32_t(((k16 >> 3) ^ ((2 + (g >> 1)) & 3)) << 4);
     {
       const char* sr = reinterpret_cast<const char*>(rslot(kt));
 #pragma unroll
@@ -196,8 +204,7 @@ struct Pipe {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           if (!tile_on(i, F)) continue;
-          const int rb = wm * WM + 32 * i + 8 * q + 4 * (g >> 1);  // first of the four rows
-          const uint32_t off = uint32_t((rb + (l16 >> 2)) * 64 + (((k16 >> 3) ^ ((rb >> 2) & 3)) << 4) + (k16 & 7) * 2);
+          const uint32_t off = ((q & 1) ? b1 : b0) + uint32_t((32 * i + 8 * q) * 64);
           const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(sr + off));
 #pragma unroll
           for (int e = 0; e < 4; ++e) acc[i][F][4 * q + e] = fmaf(id_v, bf2f(uint16_t(v[e])), acc[i][F][4 * q + e]);
@@ -355,7 +362,12 @@ __device__ __forceinline__ WavePlan diag_plan(int wave) {
     default: return {1, 3, MASK_FIRST6};
   }
 }
-__device__ __forceinline__ WavePlan full_plan(int wave) { return {wave / NWN, wave % NWN, MASK_FULL}; }
+// Full tile: the 2 x 4 grid of 128 x 64 windows, the two waves of one column
+// window (wave 2 wn and 2 wn + 1) on different SIMDs (a SIMD runs waves w and
+// w + 4): a K slice that crosses a window's identity columns (POLY) then
+// gives each SIMD one wave of identity work beside its other wave's MFMAs,
+// instead of both of one SIMD's waves while the others wait at the barrier.
+__device__ __forceinline__ WavePlan full_plan(int wave) { return {wave & 1, wave >> 1, MASK_FULL}; }
 
 template <int RK, int CK, int IDENT, int MASK, bool SHARED>
 __device__ __forceinline__ void mainloop_run(const uint16_t* rsrc_k, const uint16_t* rsrc_t, int thr_r,
@@ -698,7 +710,7 @@ __device__ __forceinline__ void px_work(const NsArgs& a, uint16_t* lds, int v) {
   f32x16 acc[TMI][TMJ];
   // acc = P X; a wave whose 64 columns all lie in the zero padding (n <= column
   // < np) computes nothing: its part of X' stays zero
-  const int wn = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) % NWN;
+  const int wn = full_plan(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)).vwn;
   mainloop<OP_SPLIT, OP_T>(P + r0 * PANEL, P + (r0 / PANEL) * pstride, r0 / BK, nullptr, X, 0, pstride, a.mp / BK,
                            lds, acc, 0.f, 0, false, c0 + wn * WN >= a.n);
 
