@@ -184,7 +184,7 @@ struct Pipe {
   // ds_read_b64_tr_b16 gives lane l of a 16-lane group the four values of one
   // column in four consecutive rows, so one read per q delivers the lane's
   // four rows.
-  template <int F>
+  template <int F, int I0 = 0, int I1 = TMI>
   __device__ __forceinline__ void ident_add(int kt, f32x16 (&acc)[TMI][TMJ]) const {
     static_assert(IDENT == IDENT_COL, "the column identity is the only one");
     const int l16 = lane & 15, g = lane >> 4;
@@ -200,7 +200,7 @@ struct Pipe {
     {
       const char* sr = reinterpret_cast<const char*>(rslot(kt));
 #pragma unroll
-      for (int i = 0; i < TMI; ++i)
+      for (int i = I0; i < I1; ++i)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           if (!tile_on(i, F)) continue;
@@ -221,7 +221,7 @@ struct Pipe {
   // kt-1, so its slot takes slice kt+NSTAGE-1; those direct loads are
   // interleaved one by one with the k step 1 MFMAs as well.  F >= 0: the
   // slice crosses this wave's identity at tile F (ident_add).
-  template <int M, int MN, int F, int RF = -1>
+  template <int M, int MN, int F, int RF = -1, int G = -1>
   __device__ __forceinline__ void body(int kt, Frags& fa, Frags& fb, f32x16 (&acc)[TMI][TMJ]) const {
     static_assert(TMI * TMJ == 8 && SLICE_DMA <= 8 && TMI + TMJ <= 8, "one read / direct load per MFMA");
 #define MMUON_MFMA(f, g)                                                                          \
@@ -234,6 +234,9 @@ struct Pipe {
     MMUON_STEP0(0) MMUON_STEP0(1) MMUON_STEP0(2) MMUON_STEP0(3)
     MMUON_STEP0(4) MMUON_STEP0(5) MMUON_STEP0(6) MMUON_STEP0(7)
 #undef MMUON_STEP0
+    // G >= 0: the second half of the identity term of slice kt-1 (tile G), whose
+    // slot is refilled only after this step's barrier
+    if constexpr (G >= 0) ident_add<G, TMI / 2, TMI>(kt - 1, acc);
     wait_vm<(NSTAGE - 3) * DMA>();  // slice kt+1; the later ones may stay in flight
     barrier();
     // on the last step slice kt+1 does not exist and the reads of its slot go
@@ -257,8 +260,9 @@ struct Pipe {
 #undef MMUON_STEP1
 #undef MMUON_MFMA
     __builtin_amdgcn_s_setprio(0);
-    // the slot of slice kt is refilled only after the next barrier
-    if constexpr (F >= 0) ident_add<F>(kt, acc);
+    // the first half of slice kt's identity term (the slot of slice kt is
+    // refilled only after the next barrier)
+    if constexpr (F >= 0) ident_add<F, 0, TMI / 2>(kt, acc);
   }
 
   // Slices a .. b-1 in form M (b > a), the last of them reading slice b in form
@@ -313,8 +317,14 @@ struct Pipe {
       const int kd = diag0 / BK;
       for (int kt = k0; kt < kd; ++kt) body<ML, ML, -1, ML>(kt, fa, fb, acc);
       body<ML, ML, 0, ML>(kd, fa, fb, acc);
-      body<ML, ML, 1, ML>(kd + 1, fa, fb, acc);
-      for (int kt = kd + TMJ; kt < KT; ++kt) body<ML, ML, -1, ML>(kt, fa, fb, acc);
+      body<ML, ML, 1, ML, 0>(kd + 1, fa, fb, acc);
+      if (kd + TMJ < KT) {
+        body<ML, ML, -1, ML, 1>(kd + TMJ, fa, fb, acc);
+        for (int kt = kd + TMJ + 1; kt < KT; ++kt) body<ML, ML, -1, ML>(kt, fa, fb, acc);
+      } else {
+        // the last slice crossed the identity; the final refills go to other slots
+        ident_add<1, TMI / 2, TMI>(KT - 1, acc);
+      }
     }
     wait_vm<0>();  // the refills of the last two steps land before the ring is reused
   }
