@@ -5,6 +5,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <cmath>
 #include <string>
 #include <vector>
 
@@ -487,6 +488,8 @@ int mmuon_adamw_fp8(const mmuon_adamw_args* a, const mmuon_adamw_fp8_tensor* met
   k.fp8 = meta;
   k.have_state = have_state ? 1 : 0;
   k.emin = expand_min;
+  k.inv_sqrt_bc2 = 1.0f / a->sqrt_bc2;
+  k.fast_quot = double(a->eps) * double(a->sqrt_bc2) >= 0x1p-37 && std::isfinite(k.inv_sqrt_bc2) ? 1 : 0;
   if (mmuon::launch_adamw_fp8(k, a->param_dtype, a->grad_dtype, a->state_dtype, v_dtype,
                               static_cast<hipStream_t>(stream)))
     return fail(MMUON_EINVAL, "unsupported FP8 AdamW dtypes param=%d grad=%d", a->param_dtype, a->grad_dtype);

@@ -34,6 +34,29 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
   p = TP::round(fmaf(a.neg_step_size, m / d, p));
 }
 
+// The same update for the FP8-state kernel, whose moments are fp32 values of a
+// format held to a tolerance, not bit for bit: the square root and the two
+// quotients use the hardware's 1-ulp v_sqrt_f32 and v_rcp_f32 (with a multiply
+// by the host's fp32 1/sqrt(bc2)) in place of the correctly rounded sequences
+// (about 30 of the kernel's 114 VALU instructions per element).  Only the
+// parameter update depends on them; the moments and their codes do not.  Used
+// where eps sqrt(bc2) >= 2^-37 (AdamWArgs::fast_quot): then d >= eps is normal,
+// and the root of a subnormal v (below 2^-63, which v_sqrt_f32 may flush to
+// zero), divided by sqrt(bc2), is below half an ulp of eps, so d + eps rounds
+// to eps either way.
+template <class TP, class TS>
+__device__ __forceinline__ void adamw_elem_fast(float& p, float g, float& m, float& v, const AdamWArgs& a) {
+  if (a.apply_wd) p = TP::round(p * a.wd_factor);
+  m = TS::round(m * a.beta1);
+  m = TS::round(fmaf(g, a.one_minus_beta1, m));
+  v = TS::round(v * a.beta2);
+  v = TS::round(fmaf(a.one_minus_beta2, g * g, v));
+  float d = TS::round(__builtin_amdgcn_sqrtf(v));
+  d = TS::round(d * a.inv_sqrt_bc2);
+  d = TS::round(d + a.eps);
+  p = TP::round(fmaf(a.neg_step_size, m * __builtin_amdgcn_rcpf(d), p));
+}
+
 constexpr int ADAM_NT = 256;
 
 template <class TP, class TG, class TS>
@@ -165,7 +188,7 @@ __device__ __forceinline__ void store_codes(uint8_t* q, int64_t e0, int nvalid, 
   }
 }
 
-template <class TP, class TG, class TS, class FM, class FV>
+template <class TP, class TG, class TS, class FM, class FV, bool FASTQ>
 __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
   const int64_t gidx = int64_t(blockIdx.x) * F8_GPW + (threadIdx.x / F8_LANES);
   if (gidx >= a.nchunks) return;  // a group's lanes leave together
@@ -203,7 +226,10 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
     for (int k = 0; k < F8_ELEMS; ++k) m[k] = v[k] = 0.f;
   }
 #pragma unroll
-  for (int k = 0; k < F8_ELEMS; ++k) adamw_elem<TP, TS>(pv[k], clipped<TG>(gv[k], a.gscale), m[k], v[k], a);
+  for (int k = 0; k < F8_ELEMS; ++k) {
+    if constexpr (FASTQ) adamw_elem_fast<TP, TS>(pv[k], clipped<TG>(gv[k], a.gscale), m[k], v[k], a);
+    else adamw_elem<TP, TS>(pv[k], clipped<TG>(gv[k], a.gscale), m[k], v[k], a);
+  }
   if (vec) {
 #pragma unroll
     for (int h = 0; h < F8_ELEMS / 8; ++h) Vec8<TP>::store(p + e0 + 8 * h, pv + 8 * h);
@@ -229,18 +255,28 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
   }
 }
 
-template <class FM, class FV>
-static int launch_adamw_fp8_f(const AdamWArgs& a, int param_dtype, int grad_dtype, hipStream_t s) {
+template <class FM, class FV, bool FASTQ>
+static int launch_adamw_fp8_q(const AdamWArgs& a, int param_dtype, int grad_dtype, hipStream_t s) {
   const dim3 grid(unsigned((a.nchunks + F8_GPW - 1) / F8_GPW)), block(ADAM_NT);
   if (param_dtype == MMUON_BF16 && grad_dtype == MMUON_BF16) {
-    if (a.have_state) hipLaunchKernelGGL((adamw_fp8_kernel<BF16T, BF16T, F32T, FM, FV>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((adamw_fp8_kernel<BF16T, BF16T, BF16T, FM, FV>), grid, block, 0, s, a);
+    if (a.have_state)
+      hipLaunchKernelGGL((adamw_fp8_kernel<BF16T, BF16T, F32T, FM, FV, FASTQ>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((adamw_fp8_kernel<BF16T, BF16T, BF16T, FM, FV, FASTQ>), grid, block, 0, s, a);
   } else if (param_dtype == MMUON_F32 && grad_dtype == MMUON_F32) {
-    hipLaunchKernelGGL((adamw_fp8_kernel<F32T, F32T, F32T, FM, FV>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((adamw_fp8_kernel<F32T, F32T, F32T, FM, FV, FASTQ>), grid, block, 0, s, a);
   } else {
     return -1;
   }
   return 0;
+}
+// the two update forms are separate kernels: with both in one kernel behind a
+// uniform branch the compiler kept 141 VGPRs live (three waves per SIMD), each
+// alone needs 110
+template <class FM, class FV>
+static int launch_adamw_fp8_f(const AdamWArgs& a, int param_dtype, int grad_dtype, hipStream_t s) {
+  return a.fast_quot ? launch_adamw_fp8_q<FM, FV, true>(a, param_dtype, grad_dtype, s)
+                     : launch_adamw_fp8_q<FM, FV, false>(a, param_dtype, grad_dtype, s);
 }
 
 int launch_adamw_fp8(const AdamWArgs& a, int param_dtype, int grad_dtype, int m_dtype, int v_dtype, hipStream_t s) {

@@ -67,6 +67,8 @@ struct AdamWArgs {
   int have_state;
   float emin;           // FP8 states: expand_min of the codec
   const float* gscale;  // gradient-clipping coefficient (device), or null
+  float inv_sqrt_bc2;   // FP8 states: fp32 1 / sqrt_bc2
+  int fast_quot;        // FP8 states: hardware root and reciprocal (eps sqrt_bc2 >= 2^-37)
 };
 int launch_adamw(const AdamWArgs& a, int param_dtype, int grad_dtype, int state_dtype,
                  hipStream_t s);

@@ -76,9 +76,15 @@ def test_ns_bf16_against_fp64_truth_and_reference(shape, form):
     truth = ns_fp64(g.cpu().to(torch.bfloat16).double())
     e_ours = rel_fro(ours, truth)
     e_ref = rel_fro(ref_bf16, truth)
-    print(f"NS {shape} {form}: ours vs fp64 {e_ours.max():.4f}, reference-bf16 vs fp64 {e_ref.max():.4f}")
+    d_ref = rel_fro(ours, ref_bf16)
+    print(f"NS {shape} {form}: ours vs fp64 {e_ours.max():.4f}, reference-bf16 vs fp64 {e_ref.max():.4f}, "
+          f"ours vs reference-bf16 {d_ref.max():.4f}")
     assert torch.all(e_ours <= 1.5 * e_ref + 2e-3), (e_ours, e_ref)
-    assert torch.all(rel_fro(ours, ref_bf16) <= 0.08)
+    # the two bf16 evaluations differ from each other by no more than their
+    # independent rounding errors explain (they add in quadrature: measured
+    # d_ref / sqrt(e_ours^2 + e_ref^2) = 0.98-1.00 on these shapes; an error of
+    # ours opposite to the reference's would approach e_ours + e_ref)
+    assert torch.all(d_ref <= 1.15 * torch.sqrt(e_ours ** 2 + e_ref ** 2) + 1e-3), (d_ref, e_ours, e_ref)
 
 
 def _spectrum_stack(m, n, spectra, seed):
