@@ -70,6 +70,7 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_kernel(AdamWArgs a) {
   const auto* g = reinterpret_cast<const typename TG::storage*>(T.grad);
   auto* m = reinterpret_cast<typename TS::storage*>(T.exp_avg);
   auto* v = reinterpret_cast<typename TS::storage*>(T.exp_avg_sq);
+  const GradClip clip = grad_clip(a.gscale);
   int64_t tail = start;
   // 8 elements per thread and 16-B accesses when all four streams are aligned
   // here; two groups' loads are issued before either is computed; every access
@@ -96,8 +97,9 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_kernel(AdamWArgs a) {
       for (int h = 0; h < 2; ++h) {
         if (h == 1 && !two) break;
         const int64_t i = h ? i1 : i0;
+        clip_grads<TG>(G[h], clip);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) adamw_elem<TP, TS>(P[h][e], clipped<TG>(G[h][e], a.gscale), M[h][e], V[h][e], a);
+        for (int e = 0; e < 8; ++e) adamw_elem<TP, TS>(P[h][e], G[h][e], M[h][e], V[h][e], a);
         Vec8<TP>::store_nt(p + i, P[h]);
         Vec8<TS>::store_nt(m + i, M[h]);
         Vec8<TS>::store_nt(v + i, V[h]);
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_kernel(AdamWArgs a) {
   }
   for (int64_t i = tail + threadIdx.x; i < end; i += ADAM_NT) {
     float pv = TP::load(p, i), mv = TS::load(m, i), vv = TS::load(v, i);
-    adamw_elem<TP, TS>(pv, clipped<TG>(TG::load(g, i), a.gscale), mv, vv, a);
+    adamw_elem<TP, TS>(pv, clipped<TG>(TG::load(g, i), clip), mv, vv, a);
     TP::store(p, i, pv);
     TS::store(m, i, mv);
     TS::store(v, i, vv);
@@ -213,6 +215,7 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
   float pv[F8_ELEMS], gv[F8_ELEMS], m[F8_ELEMS], v[F8_ELEMS];
   load_lane<TP>(p, e0, nvalid, vec, pv);
   load_lane<TG>(g, e0, nvalid, vec, gv);
+  clip_grads<TG>(gv, grad_clip(a.gscale));
   if (a.have_state) {
     uint4 cm[F8_ELEMS / 16], cv[F8_ELEMS / 16];
     load_codes(qm, e0, nvalid, vec, cm);
@@ -227,8 +230,8 @@ __global__ __launch_bounds__(ADAM_NT) void adamw_fp8_kernel(AdamWArgs a) {
   }
 #pragma unroll
   for (int k = 0; k < F8_ELEMS; ++k) {
-    if constexpr (FASTQ) adamw_elem_fast<TP, TS>(pv[k], clipped<TG>(gv[k], a.gscale), m[k], v[k], a);
-    else adamw_elem<TP, TS>(pv[k], clipped<TG>(gv[k], a.gscale), m[k], v[k], a);
+    if constexpr (FASTQ) adamw_elem_fast<TP, TS>(pv[k], gv[k], m[k], v[k], a);
+    else adamw_elem<TP, TS>(pv[k], gv[k], m[k], v[k], a);
   }
   if (vec) {
 #pragma unroll

@@ -142,7 +142,7 @@ constexpr int P_GPW = F8_NT / PL;  // 128-groups per workgroup
 // foreach ops round.
 template <class TG, class F>
 __device__ __forceinline__ void fp8_momentum_lane(const uint8_t* q, const mmuon_block_fp8& md, int64_t grp,
-                                                  int64_t e0, const typename TG::storage* g, const float* gscale,
+                                                  int64_t e0, const typename TG::storage* g, GradClip clip,
                                                   float mu, int have_state, float (&nv)[PE]) {
   float old[PE];
   if (have_state) {
@@ -157,10 +157,11 @@ __device__ __forceinline__ void fp8_momentum_lane(const uint8_t* q, const mmuon_
   float gv[PE];
 #pragma unroll
   for (int h = 0; h < PE / 8; ++h) Vec8<TG>::load(g + e0 + 8 * h, gv + 8 * h);
+  clip_grads<TG>(gv, clip);
 #pragma unroll
   for (int k = 0; k < PE; ++k) {
     const float t = old[k] * mu;
-    nv[k] = t + clipped<TG>(gv[k], gscale);
+    nv[k] = t + gv[k];
   }
 }
 
@@ -225,7 +226,7 @@ __global__ __launch_bounds__(F8_NT) void fp8_pack_rows_kernel(PackArgs a, const 
   if (grp < gpb) {  // uniform over the group's lanes
     const int64_t e0 = grp * 128 + (threadIdx.x % PL) * PE;
     float nv[PE];
-    fp8_momentum_lane<TG, F>(q, md, grp, e0, g, a.gscale, a.mu, have_state, nv);
+    fp8_momentum_lane<TG, F>(q, md, grp, e0, g, grad_clip(a.gscale), a.mu, have_state, nv);
     if (!TRANS && cols % PE == 0) {
       // PE elements of one row, inside one 32-column panel (a block is below
       // 2^31 elements)
@@ -272,7 +273,7 @@ __global__ __launch_bounds__(F8_NT) void fp8_pack_cols_kernel(PackArgs a, const 
   if (r < rows) {  // uniform over the group's lanes
     const int64_t e0 = int64_t(r) * cols + c0 + sub * PE;
     const int64_t grp = e0 >> 7;
-    fp8_momentum_lane<TG, F>(q, md, grp, e0, g, a.gscale, a.mu, have_state, nv);
+    fp8_momentum_lane<TG, F>(q, md, grp, e0, g, grad_clip(a.gscale), a.mu, have_state, nv);
     fp8_store_group<F>(q, md, grp, e0, nv, emin);
   }
 #pragma unroll

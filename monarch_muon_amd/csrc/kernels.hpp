@@ -90,10 +90,28 @@ size_t butterfly_workspace(const mmuon_butterfly_args& a);
 int launch_butterfly_fwd(const mmuon_butterfly_args& a, hipStream_t s);
 int launch_butterfly_bwd(const mmuon_butterfly_args& a, hipStream_t s);
 
+// Gradient-clipping coefficient of a launch (gscale: device pointer, or null
+// when not clipping), read once per thread: the per-element form would test
+// the pointer in every element (a branch each) and, after the thread's first
+// store, reload the coefficient with a wait on every memory access in flight.
+struct GradClip {
+  bool on;
+  float c;
+};
+__device__ __forceinline__ GradClip grad_clip(const float* gscale) {
+  return gscale != nullptr ? GradClip{true, *gscale} : GradClip{false, 1.f};
+}
 // Gradient as the step reads it: dtype(g * c) when clipping, else g.
 template <class TG>
-__device__ __forceinline__ float clipped(float g, const float* gscale) {
-  return gscale != nullptr ? TG::round(g * *gscale) : g;
+__device__ __forceinline__ float clipped(float g, GradClip k) {
+  return k.on ? TG::round(g * k.c) : g;
+}
+template <class TG, int N>
+__device__ __forceinline__ void clip_grads(float (&g)[N], GradClip k) {
+  if (k.on) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) g[i] = TG::round(g[i] * k.c);
+  }
 }
 
 // FP8 codec (fp8_dtype: MMUON_F8E4M3 or MMUON_F8E5M2; emin: expand_min) -------

@@ -41,6 +41,7 @@ __global__ __launch_bounds__(PACK_NT) void pack_rows_kernel(PackArgs a) {
   const int64_t total = int64_t(a.mp) * a.np;
   const int tiles_j = a.np / 256;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const GradClip clip = grad_clip(a.gscale);
   float ss = 0.f;
   if constexpr (PANELS) {
     const int i = (blockIdx.x / tiles_j) * 32 + wave * 8 + (lane >> 3);
@@ -58,9 +59,10 @@ __global__ __launch_bounds__(PACK_NT) void pack_rows_kernel(PackArgs a) {
 #pragma unroll
       for (int it = 0; it < PACK_ITERS; ++it) {
         float v[8];
+        clip_grads<TG>(gv[it], clip);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-          bv[it][q] = momentum_update<TB>(bv[it][q], clipped<TG>(gv[it][q], a.gscale), a.mu);
+          bv[it][q] = momentum_update<TB>(bv[it][q], gv[it][q], a.mu);
           v[q] = TX::round(bv[it][q]);
           ss += v[q] * v[q];
         }
@@ -91,8 +93,9 @@ __global__ __launch_bounds__(PACK_NT) void pack_rows_kernel(PackArgs a) {
       float gv[8], bv[8];
       Vec8<TG>::load(g + s, gv);
       Vec8<TB>::load(buf + s, bv);
+      clip_grads<TG>(gv, clip);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) bv[q] = momentum_update<TB>(bv[q], clipped<TG>(gv[q], a.gscale), a.mu);
+      for (int q = 0; q < 8; ++q) bv[q] = momentum_update<TB>(bv[q], gv[q], a.mu);
       Vec8<TB>::store(buf + s, bv);
 #pragma unroll
       for (int q = 0; q < 8; ++q) v[q] = TX::round(bv[q]);
@@ -102,7 +105,7 @@ __global__ __launch_bounds__(PACK_NT) void pack_rows_kernel(PackArgs a) {
         v[q] = 0.f;
         if (i < a.m && j + q < a.n) {
           const int64_t s = int64_t(i) * a.n + j + q;
-          const float nb = momentum_update<TB>(TB::load(buf, s), clipped<TG>(TG::load(g, s), a.gscale), a.mu);
+          const float nb = momentum_update<TB>(TB::load(buf, s), clipped<TG>(TG::load(g, s), clip), a.mu);
           TB::store(buf, s, nb);
           v[q] = TX::round(nb);
         }
@@ -138,6 +141,7 @@ __global__ __launch_bounds__(PACK_NT) void pack_cols_kernel(PackArgs a) {
   const auto* g = reinterpret_cast<const typename TG::storage*>(ref.grad);
   auto* buf = reinterpret_cast<typename TB::storage*>(ref.buf);
   auto* x = reinterpret_cast<typename TX::storage*>(a.x) + int64_t(b) * a.mp * a.np;
+  const GradClip clip = grad_clip(a.gscale);
   float ss = 0.f;
   // phase 1: chunk e = q * PACK_NT + t covers buf row r0 + e/32, columns c0 + 8 (e%32) + [0, 8)
   if (a.vec && r0 + PCOL_ROWS <= a.n && c0 + PCOL_COLS <= a.m) {
@@ -149,6 +153,10 @@ __global__ __launch_bounds__(PACK_NT) void pack_cols_kernel(PackArgs a) {
       Vec8<TG>::load(g + s, gv[q]);
       Vec8<TB>::load(buf + s, bv[q]);
     }
+    if (clip.on) {
+#pragma unroll
+      for (int q = 0; q < CHUNKS; ++q) clip_grads<TG>(gv[q], clip);
+    }
 #pragma unroll
     for (int q = 0; q < CHUNKS; ++q) {
       const int e = q * PACK_NT + threadIdx.x;
@@ -156,7 +164,7 @@ __global__ __launch_bounds__(PACK_NT) void pack_cols_kernel(PackArgs a) {
       float v[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        bv[q][k] = momentum_update<TB>(bv[q][k], clipped<TG>(gv[q][k], a.gscale), a.mu);
+        bv[q][k] = momentum_update<TB>(bv[q][k], gv[q][k], a.mu);
         v[k] = TX::round(bv[q][k]);
         ss += v[k] * v[k];
       }
@@ -175,7 +183,7 @@ __global__ __launch_bounds__(PACK_NT) void pack_cols_kernel(PackArgs a) {
         float v = 0.f;
         if (r < a.n && c + k < a.m) {
           const int64_t s = int64_t(r) * a.m + c + k;
-          const float nb = momentum_update<TB>(TB::load(buf, s), clipped<TG>(TG::load(g, s), a.gscale), a.mu);
+          const float nb = momentum_update<TB>(TB::load(buf, s), clipped<TG>(TG::load(g, s), clip), a.mu);
           TB::store(buf, s, nb);
           v = TX::round(nb);
         }
