@@ -267,6 +267,37 @@ def test_fp8_state_formats_and_expand_min_against_oracle(first, second, emin):
               f"{max(s['code_mismatch'] for _, s in stats):.2e}")
 
 
+@pytest.mark.parametrize("eps", [1e-8, 1e-20], ids=["hardware-root", "exact-root"])
+def test_fp8_adamw_update_forms_against_oracle(eps):
+    """The FP8-state AdamW's two forms of the parameter update: the hardware's
+    1-ulp square root and reciprocal (taken where eps sqrt(1 - beta2^t) >=
+    2^-37, so with the default eps) and the correctly rounded ones (a tiny
+    eps).  fp32 parameters, three steps of the toy's AdamW tensors against the
+    oracle at the fp32 weights bar, codes as in the other tests."""
+    w, draws = _workload_params("toy", None, 256)
+    gm, ga = _params(draws, torch.float32)
+    cm, ca = _params(draws, torch.float32)
+    gopt = CoatStateMonarchMuon(gm, ga, lr=0.02, momentum=0.95, adamw_eps=eps, qargs=QuantizationConfig(),
+                                ns_dtype=None)
+    copt = ReferenceCoatStateMonarchMuon(cm, ca, lr=0.02, momentum=0.95, adamw_eps=eps, variant="pretrain")
+    copt.keep_values = True
+    for step in range(3):
+        if step:
+            _sync(gm + ga, gopt, cm + ca, copt)
+        copt.step()
+        gopt.step()
+        torch.cuda.synchronize()
+        stats, worst = [], 0.0
+        for p, q in zip(gm + ga, cm + ca):
+            e = blocks_rel(p, q).max().item()
+            worst = max(worst, e)
+            assert e <= F32_TOL, (step, e)
+            for sname, signed in FP8_STATES.items():
+                if sname in copt.values.get(q, {}):
+                    _compare_codes(gopt.state[p], sname, copt.values[q][sname], signed, stats=stats)
+        print(f"AdamW eps {eps:g} step {step + 1}: worst weight error {worst:.3e} (bar {F32_TOL})")
+
+
 @pytest.mark.parametrize("variant,dtype", [("pretrain", torch.float32), ("membench", torch.bfloat16)])
 def test_fp8_states_with_groups_straddling_blocks_against_oracle(variant, dtype):
     """Monarch factors whose blocks hold a number of elements that is not a
