@@ -849,12 +849,12 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void ns_px_bf16(NsArgs a, int total)
 // fp32 Newton-Schulz (the pretrain copy keeps the buffer dtype) on the fp32
 // matrix cores (v_mfma_f32_32x32x2_f32, fp32 products and accumulation).
 // 128 x 128 output tiles per 256-thread workgroup, 4 waves of 64 x 64 (2 x 2
-// MFMA tiles of 32 x 32, 64 MFMAs per wave and K tile); K advances 32 per
+// MFMA tiles of 32 x 32, 32 MFMAs per wave and K tile); K advances 16 per
 // tile, double-buffered in LDS: the next tile's global loads (into registers)
 // are in flight during the current tile's MFMAs and stored to the other buffer
-// after them.  Operands reach LDS in one of two forms:
+// part way through them.  Operands reach LDS in one of two forms:
 //   RK: operand rows, [row][k] (rows of X for SYRK; rows of A / P, and by
-//       symmetry A's columns), 33 floats per row, so the 32 lanes that read
+//       symmetry A's columns), 17 floats per row, so the 32 lanes that read
 //       one k of 32 consecutive rows hit 32 different banks;
 //   KC: [k][col] (PX's X operand, k = rows of X), 132 floats per row, 16-B
 //       aligned for float4 stores.
@@ -863,45 +863,48 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void ns_px_bf16(NsArgs a, int total)
 // stores are row-contiguous), so the stored matrix is exactly symmetric.
 // ---------------------------------------------------------------------------
 constexpr int FT = 128;                // output tile
-constexpr int FK = 32;                 // K tile
+constexpr int FK = 16;                 // K tile
 constexpr int F_NT = 256;              // 4 waves, 2 x 2
 constexpr int RK_LD = FK + 1;
 constexpr int KC_LD = FT + 4;
 constexpr int F_OPER = FT * RK_LD;     // floats per operand buffer
-static_assert(FK * KC_LD == F_OPER, "both forms fill one operand buffer");
+static_assert(FK * KC_LD <= F_OPER, "both forms fit one operand buffer");
 constexpr int F_ST = FT + 1;           // staged tile: 129 floats per row
-constexpr int F_APPLY_BATCH = 16;      // parameter elements per batch of the apply's loads
-constexpr int F_STORE_KK = 11;         // k step after whose MFMAs the next K tile is written to LDS
-static_assert(FT * F_ST <= 4 * F_OPER, "the staged tile fits in the operand buffers");
+constexpr int F_HALF = FT / 2;         // the tile is staged and stored half its rows at a time
+static_assert(F_HALF * F_ST <= 4 * F_OPER, "half the staged tile fits in the operand buffers");
+constexpr int F_APPLY_BATCH = 8;       // parameter elements per batch of the apply's loads
+constexpr int F_STORE_KK = 5;          // k step after whose MFMAs the next K tile is written to LDS
+constexpr int F_RQ = FK / 4;           // float4 per operand row of a K tile
+constexpr int F_QPT = FT * FK / 4 / F_NT;  // float4 per thread and operand K tile
 
-// One operand's K tile in registers: 1024 float4, four per thread.
+// One operand's K tile in registers.
 struct F32Stage {
-  float4 v[4];
+  float4 v[F_QPT];
 };
 
-// rows r0 .. r0+127 of a row-major matrix (leading dimension ld), k0 .. k0+31
+// rows r0 .. r0+127 of a row-major matrix (leading dimension ld), k0 .. k0+FK-1
 __device__ __forceinline__ void f32_load_rows(F32Stage& g, const float* src, int64_t ld, int r0, int k0) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < F_QPT; ++j) {
     const int idx = threadIdx.x + F_NT * j;
-    g.v[j] = *reinterpret_cast<const float4*>(src + int64_t(r0 + (idx >> 3)) * ld + k0 + 4 * (idx & 7));
+    g.v[j] = *reinterpret_cast<const float4*>(src + int64_t(r0 + idx / F_RQ) * ld + k0 + 4 * (idx % F_RQ));
   }
 }
 __device__ __forceinline__ void f32_store_rk(const F32Stage& g, float* s) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < F_QPT; ++j) {
     const int idx = threadIdx.x + F_NT * j;
-    float* d = s + (idx >> 3) * RK_LD + 4 * (idx & 7);
+    float* d = s + (idx / F_RQ) * RK_LD + 4 * (idx % F_RQ);
     d[0] = g.v[j].x;
     d[1] = g.v[j].y;
     d[2] = g.v[j].z;
     d[3] = g.v[j].w;
   }
 }
-// rows k0 .. k0+31 of X (leading dimension ld), columns c0 .. c0+127
+// rows k0 .. k0+FK-1 of X (leading dimension ld), columns c0 .. c0+127
 __device__ __forceinline__ void f32_load_kc(F32Stage& g, const float* X, int64_t ld, int c0, int k0) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < F_QPT; ++j) {
     const int idx = threadIdx.x + F_NT * j;
     g.v[j] = *reinterpret_cast<const float4*>(X + int64_t(k0 + (idx >> 5)) * ld + c0 + 4 * (idx & 31));
   }
@@ -911,7 +914,7 @@ __device__ __forceinline__ void f32_store_kc(const F32Stage& g, float* s) {
   // tile in scratch memory)
   typedef float f32x4_t __attribute__((ext_vector_type(4)));
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < F_QPT; ++j) {
     const int idx = threadIdx.x + F_NT * j;
     const f32x4_t v = {g.v[j].x, g.v[j].y, g.v[j].z, g.v[j].w};
     *reinterpret_cast<f32x4_t*>(s + (idx >> 5) * KC_LD + 4 * (idx & 31)) = v;
@@ -931,15 +934,15 @@ __device__ __forceinline__ void f32_sym_tile(int t, int nt, int& ti, int& tj) {
 }
 
 // Add v to the diagonal entries of an RK-form K tile in registers: rows rbase
-// + 0..127 of the operand, k0 .. k0+31; an element is on the diagonal when its
-// row equals its k.  The quintic's linear terms enter the products this way:
-// PX multiplies (P + a I) X, POLY A (A + (b/c) I); no epilogue reads global
-// memory and no accumulator leaves the matrix registers.
+// + 0..127 of the operand, k0 .. k0+FK-1; an element is on the diagonal when
+// its row equals its k.  The quintic's linear terms enter the products this
+// way: PX multiplies (P + a I) X, POLY A (A + (b/c) I); no epilogue reads
+// global memory and no accumulator leaves the matrix registers.
 __device__ __forceinline__ void f32_add_diag(F32Stage& g, int rbase, int k0, float v) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < F_QPT; ++j) {
     const int idx = threadIdx.x + F_NT * j;
-    const int d = rbase + (idx >> 3) - (k0 + 4 * (idx & 7));  // row - k of the float4's first element
+    const int d = rbase + idx / F_RQ - (k0 + 4 * (idx % F_RQ));  // row - k of the float4's first element
     if (d == 0) g.v[j].x += v;
     if (d == 1) g.v[j].y += v;
     if (d == 2) g.v[j].z += v;
@@ -947,8 +950,12 @@ __device__ __forceinline__ void f32_add_diag(F32Stage& g, int rbase, int k0, flo
   }
 }
 
+// 16-deep K tiles double-buffered in 35 KiB of LDS, so three workgroups share a
+// CU (three waves per SIMD, which hide each other's barrier and load waits).
+// The 128 x 128 output tile is staged and stored in two halves of 64 rows (the
+// rows of one wave row, wr), each in the operand buffers.
 template <int STAGE, class TP>
-__global__ __launch_bounds__(F_NT) void ns_f32(NsArgs a) {
+__global__ __launch_bounds__(F_NT) __attribute__((amdgpu_waves_per_eu(3))) void ns_f32(NsArgs a) {
   __shared__ __attribute__((aligned(16))) float lds[4 * F_OPER];  // [buffer 0: A, B][buffer 1: A, B]
   constexpr bool PX = STAGE == NS_PX || STAGE == NS_PX_APPLY;
   constexpr bool SYM = STAGE == NS_SYRK || STAGE == NS_POLY;
@@ -995,8 +1002,7 @@ __global__ __launch_bounds__(F_NT) void ns_f32(NsArgs a) {
     }
     // 32x32x2 steps: lane l supplies row (column) l%32 at k = 2 kk + l/32.
     // The next K tile is written to the other buffer after the MFMAs of k step
-    // F_STORE_KK, so its LDS writes issue while this tile's MFMAs still run
-    // (PX 2% faster than writing it after the last k step).
+    // F_STORE_KK, so its LDS writes issue while this tile's MFMAs still run.
     const bool more = t + 1 < KT;
 #pragma unroll
     for (int kk = 0; kk < FK / 2; ++kk) {
@@ -1022,76 +1028,95 @@ __global__ __launch_bounds__(F_NT) void ns_f32(NsArgs a) {
     }
     __syncthreads();
   }
-  // stage the tile: accumulator value 4 q + e of MFMA tile (i, j) holds row
-  // 64 wr + 32 i + 8 q + 4 (lane/32) + e, column 64 wc + 32 j + lane%32
-  float* T = lds;
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = wr * 64 + i * 32 + 8 * q + 4 * (lane >> 5) + e, c = wc * 64 + j * 32 + (lane & 31);
-          T[r * F_ST + c] = acc[i][j][4 * q + e];
-        }
-  __syncthreads();
   const float s = a.scale != nullptr ? a.scale[b] : 1.f;
-  // element idx of the tile, two mappings (consecutive lanes along the
-  // destination's rows): direct (r, c) = (idx / 128, idx % 128) and mirrored
-  // (r, c) = (idx % 128, idx / 128), the latter for stores along a column of
-  // the tile (a symmetric mirror, a tall block's parameter rows)
-  if (STAGE == NS_SYRK || STAGE == NS_POLY) {
-    // SYRK: A = s^2 acc; POLY: P = c (A A + (b/c) A) = b A + c A A
-    float* out = static_cast<float*>(a.out) + int64_t(b) * a.mp * a.mp;
-    const float f = STAGE == NS_SYRK ? s * s : a.cc;
-    for (int it = 0; it < FT * FT / F_NT; ++it) {
-      const int idx = threadIdx.x + F_NT * it, r = idx >> 7, c = idx & 127;
-      // a diagonal tile takes its lower triangle from the upper one
-      const float v = (tj == ti && r > c) ? T[c * F_ST + r] : T[r * F_ST + c];
-      out[int64_t(r0 + r) * a.mp + c0 + c] = v * f;
+  const bool diag = SYM && tj == ti;
+  float* T = lds;  // T[r - 64 h][c]: rows 64 h .. 64 h + 63 of the tile
+  auto* prm = STAGE == NS_PX_APPLY ? reinterpret_cast<typename TP::storage*>(a.blocks[b].param) : nullptr;
+#pragma unroll 1
+  for (int h = 0; h < 2; ++h) {
+    if (h) __syncthreads();  // every wave is done reading the first half
+    // stage half h: accumulator value 4 q + e of MFMA tile (i, j) holds row
+    // 64 wr + 32 i + 8 q + 4 (lane/32) + e, column 64 wc + 32 j + lane%32, so
+    // the waves with wr == h hold the half
+    if (wr == h) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int r = i * 32 + 8 * q + 4 * (lane >> 5) + e, c = wc * 64 + j * 32 + (lane & 31);
+              T[r * F_ST + c] = acc[i][j][4 * q + e];
+            }
     }
-    if (tj != ti) {
-      for (int it = 0; it < FT * FT / F_NT; ++it) {
-        const int idx = threadIdx.x + F_NT * it, r = idx & 127, c = idx >> 7;
-        out[int64_t(c0 + c) * a.mp + r0 + r] = T[r * F_ST + c] * f;  // the mirror of (r0 + r, c0 + c)
+    __syncthreads();
+    // element idx of the half, two mappings (consecutive lanes along the
+    // destination's rows): direct (r, c) = (64 h + idx / 128, idx % 128) and
+    // mirrored (r, c) = (64 h + idx % 64, idx / 64), the latter for stores
+    // along a column of the tile (a symmetric mirror, a tall block's
+    // parameter rows)
+    constexpr int PER = F_HALF * FT / F_NT;  // elements per thread and half
+    if constexpr (SYM) {
+      // SYRK: A = s^2 acc; POLY: P = c (A A + (b/c) A) = b A + c A A.  A
+      // diagonal tile takes its lower triangle from the upper one: in the
+      // first half from T[c][r] (c < r < 64) and, for the 64 x 64 block
+      // below it, from the first half's mirror stores; in the second half
+      // from T[c][r] (64 <= c < r).
+      float* out = static_cast<float*>(a.out) + int64_t(b) * a.mp * a.mp;
+      const float f = STAGE == NS_SYRK ? s * s : a.cc;
+#pragma unroll 4
+      for (int it = 0; it < PER; ++it) {
+        const int idx = threadIdx.x + F_NT * it, rl = idx >> 7, c = idx & 127, r = F_HALF * h + rl;
+        if (diag && c < F_HALF * h) continue;
+        const float v = (diag && r > c) ? T[(c - F_HALF * h) * F_ST + r] : T[rl * F_ST + c];
+        out[int64_t(r0 + r) * a.mp + c0 + c] = v * f;
       }
-    }
-    return;
-  }
-  if (STAGE == NS_PX) {  // X' = s (a X + P X)
-    float* out = static_cast<float*>(a.out) + int64_t(b) * a.mp * a.np;
-    for (int it = 0; it < FT * FT / F_NT; ++it) {
-      const int idx = threadIdx.x + F_NT * it, r = idx >> 7, c = idx & 127;
-      out[int64_t(r0 + r) * a.np + c0 + c] = s * T[r * F_ST + c];
-    }
-    return;
-  }
-  // PX_APPLY: param += alpha X' (un-transposed); the block is (m x n) or, tall, (n x m).
-  // F_APPLY_BATCH elements per batch: their parameter loads are all issued
-  // before the first update is stored, so a thread waits for the load latency
-  // once per batch rather than once per element.
-  auto* prm = reinterpret_cast<typename TP::storage*>(a.blocks[b].param);
-  constexpr int PB = F_APPLY_BATCH;
-  static_assert((FT * FT / F_NT) % PB == 0, "whole batches per thread");
-  for (int it0 = 0; it0 < FT * FT / F_NT; it0 += PB) {
-    float pv[PB];
-    int64_t off[PB];
+      if (!diag || h == 0) {
+#pragma unroll 4
+        for (int it = 0; it < PER; ++it) {
+          const int idx = threadIdx.x + F_NT * it, rl = idx & (F_HALF - 1), c = idx / F_HALF, r = F_HALF * h + rl;
+          if (diag && c < F_HALF) continue;
+          out[int64_t(c0 + c) * a.mp + r0 + r] = T[rl * F_ST + c] * f;  // the mirror of (r0 + r, c0 + c)
+        }
+      }
+    } else if constexpr (STAGE == NS_PX) {  // X' = s (a X + P X)
+      float* out = static_cast<float*>(a.out) + int64_t(b) * a.mp * a.np;
+#pragma unroll 4
+      for (int it = 0; it < PER; ++it) {
+        const int idx = threadIdx.x + F_NT * it, rl = idx >> 7, c = idx & 127;
+        out[int64_t(r0 + F_HALF * h + rl) * a.np + c0 + c] = s * T[rl * F_ST + c];
+      }
+    } else {
+      // PX_APPLY: param += alpha X' (un-transposed); the block is (m x n) or,
+      // tall, (n x m).  F_APPLY_BATCH elements per batch: their parameter loads
+      // are all issued before the first update is stored, so a thread waits
+      // for the load latency once per batch rather than once per element.
+      constexpr int PB = F_APPLY_BATCH;
+      static_assert(PER % PB == 0, "whole batches per thread");
+#pragma unroll 1
+      for (int it0 = 0; it0 < PER; it0 += PB) {
+        float pv[PB];
+        int64_t off[PB];
 #pragma unroll
-    for (int q = 0; q < PB; ++q) {
-      const int idx = threadIdx.x + F_NT * (it0 + q);
-      const int r = a.transposed ? (idx & 127) : (idx >> 7), c = a.transposed ? (idx >> 7) : (idx & 127);
-      const int i = r0 + r, j = c0 + c;
-      off[q] = i < a.m && j < a.n ? (a.transposed ? int64_t(j) * a.m + i : int64_t(i) * a.n + j) : -1;
-      pv[q] = off[q] >= 0 ? TP::load(prm, off[q]) : 0.f;
-    }
+        for (int q = 0; q < PB; ++q) {
+          const int idx = threadIdx.x + F_NT * (it0 + q);
+          const int rl = a.transposed ? (idx & (F_HALF - 1)) : (idx >> 7);
+          const int c = a.transposed ? (idx / F_HALF) : (idx & 127);
+          const int i = r0 + F_HALF * h + rl, j = c0 + c;
+          off[q] = i < a.m && j < a.n ? (a.transposed ? int64_t(j) * a.m + i : int64_t(i) * a.n + j) : -1;
+          pv[q] = off[q] >= 0 ? TP::load(prm, off[q]) : 0.f;
+        }
 #pragma unroll
-    for (int q = 0; q < PB; ++q) {
-      if (off[q] < 0) continue;
-      const int idx = threadIdx.x + F_NT * (it0 + q);
-      const int r = a.transposed ? (idx & 127) : (idx >> 7), c = a.transposed ? (idx >> 7) : (idx & 127);
-      TP::store(prm, off[q], fmaf(a.alpha, s * T[r * F_ST + c], pv[q]));
+        for (int q = 0; q < PB; ++q) {
+          if (off[q] < 0) continue;
+          const int idx = threadIdx.x + F_NT * (it0 + q);
+          const int rl = a.transposed ? (idx & (F_HALF - 1)) : (idx >> 7);
+          const int c = a.transposed ? (idx / F_HALF) : (idx & 127);
+          TP::store(prm, off[q], fmaf(a.alpha, s * T[rl * F_ST + c], pv[q]));
+        }
+      }
     }
   }
 }
