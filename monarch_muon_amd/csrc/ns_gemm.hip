@@ -852,7 +852,7 @@ __global__ __launch_bounds__(NT, WG_PER_CU) void ns_px_bf16(NsArgs a, int total)
 // MFMA tiles of 32 x 32, 32 MFMAs per wave and K tile); K advances 16 per
 // tile, double-buffered in LDS: the next tile's global loads (into registers)
 // are in flight during the current tile's MFMAs and stored to the other buffer
-// part way through them.  Operands reach LDS in one of two forms:
+// after them.  Operands reach LDS in one of two forms:
 //   RK: operand rows, [row][k] (rows of X for SYRK; rows of A / P, and by
 //       symmetry A's columns), 17 floats per row, so the 32 lanes that read
 //       one k of 32 consecutive rows hit 32 different banks;
@@ -873,7 +873,6 @@ constexpr int F_ST = FT + 1;           // staged tile: 129 floats per row
 constexpr int F_HALF = FT / 2;         // the tile is staged and stored half its rows at a time
 static_assert(F_HALF * F_ST <= 4 * F_OPER, "half the staged tile fits in the operand buffers");
 constexpr int F_APPLY_BATCH = 8;       // parameter elements per batch of the apply's loads
-constexpr int F_STORE_KK = 5;          // k step after whose MFMAs the next K tile is written to LDS
 constexpr int F_RQ = FK / 4;           // float4 per operand row of a K tile
 constexpr int F_QPT = FT * FK / 4 / F_NT;  // float4 per thread and operand K tile
 
@@ -1000,10 +999,7 @@ __global__ __launch_bounds__(F_NT) __attribute__((amdgpu_waves_per_eu(3))) void 
       if (PX) f32_load_kc(gb, X, a.np, c0, (t + 1) * FK);
       else f32_load_rows(gb, rsrc, rld, c0, (t + 1) * FK);
     }
-    // 32x32x2 steps: lane l supplies row (column) l%32 at k = 2 kk + l/32.
-    // The next K tile is written to the other buffer after the MFMAs of k step
-    // F_STORE_KK, so its LDS writes issue while this tile's MFMAs still run.
-    const bool more = t + 1 < KT;
+    // 32x32x2 steps: lane l supplies row (column) l%32 at k = 2 kk + l/32
 #pragma unroll
     for (int kk = 0; kk < FK / 2; ++kk) {
       const int k = 2 * kk + (lane >> 5);
@@ -1017,14 +1013,14 @@ __global__ __launch_bounds__(F_NT) __attribute__((amdgpu_waves_per_eu(3))) void 
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
-      if (kk == F_STORE_KK && more) {
-        float* d = lds + ((t + 1) & 1) * 2 * F_OPER;
-        if (PX) f32_add_diag(ga, r0, (t + 1) * FK, a.ca);
-        if (STAGE == NS_POLY) f32_add_diag(gb, c0, (t + 1) * FK, a.cb / a.cc);
-        f32_store_rk(ga, d);
-        if (PX) f32_store_kc(gb, d + F_OPER);
-        else f32_store_rk(gb, d + F_OPER);
-      }
+    }
+    if (t + 1 < KT) {
+      float* d = lds + ((t + 1) & 1) * 2 * F_OPER;
+      if (PX) f32_add_diag(ga, r0, (t + 1) * FK, a.ca);
+      if (STAGE == NS_POLY) f32_add_diag(gb, c0, (t + 1) * FK, a.cb / a.cc);
+      f32_store_rk(ga, d);
+      if (PX) f32_store_kc(gb, d + F_OPER);
+      else f32_store_rk(gb, d + F_OPER);
     }
     __syncthreads();
   }
