@@ -38,8 +38,9 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
 // format held to a tolerance, not bit for bit: the square root and the two
 // quotients use the hardware's 1-ulp v_sqrt_f32 and v_rcp_f32 (with a multiply
 // by the host's fp32 1/sqrt(bc2)) in place of the correctly rounded sequences
-// (about 30 of the kernel's 114 VALU instructions per element).  Only the
-// parameter update depends on them; the moments and their codes do not.  Used
+// (the kernel issues 77 VALU instructions per element with them, 114 without).
+// Only the parameter update depends on them; the moments and their codes do
+// not.  Used
 // where eps sqrt(bc2) >= 2^-37 (AdamWArgs::fast_quot): then d >= eps is normal,
 // and the root of a subnormal v (below 2^-63, which v_sqrt_f32 may flush to
 // zero), divided by sqrt(bc2), is below half an ulp of eps, so d + eps rounds
