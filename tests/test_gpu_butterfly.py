@@ -35,6 +35,7 @@ CASES = [
     (1, 4, 256, 256, 256),
     (300, 1, 256, 512, 384),      # one block: the riffle is the identity
     (200, 8, 256, 256, 264),      # eight blocks: 32-column planes, s not a multiple of 16
+    (200, 16, 512, 256, 520),     # sixteen blocks (the most the kernels take): 16-column planes
 ]
 
 
