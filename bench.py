@@ -594,7 +594,14 @@ def main():
                     help="summarise rocprofv3 counter CSVs (SQ_INSTS_MFMA, SQ_VALU_MFMA_BUSY_CYCLES, "
                          "GRBM_GUI_ACTIVE; or SQ_INSTS_VALU, SQ_INSTS_VALU_TRANS_F32, SQ_INSTS_VMEM, "
                          "SQ_INSTS_LDS) into OUT_JSON")
+    ap.add_argument("--stall-summary", nargs=2, metavar=("OUT_JSON", "CSV"),
+                    help="summarise a rocprofv3 counter CSV (SQ_WAVE_CYCLES, SQ_WAIT_ANY, SQ_WAIT_INST_ANY, "
+                         "SQ_LDS_BANK_CONFLICT, SQ_INSTS_LDS) into OUT_JSON: where each kernel's waves wait")
     args = ap.parse_args()
+    if args.stall_summary:
+        import bench_studies
+        bench_studies.stall_summary(args)
+        return
     if args.mfma_summary:
         import bench_studies
         bench_studies.mfma_summary(args)

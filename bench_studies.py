@@ -629,3 +629,29 @@ def mfma_summary(args):
         res[k] = rec
     Path(out_path).write_text(json.dumps({"simds": simds, "kernels": res}, indent=1) + "\n")
     print(json.dumps(res, indent=1))
+
+
+def stall_summary(args):
+    """Where each kernel's waves wait, from a rocprofv3 counter run
+    (``--stall-summary OUT.json CSV``; counters SQ_WAVES, SQ_WAVE_CYCLES,
+    SQ_WAIT_ANY, SQ_WAIT_INST_ANY, SQ_BUSY_CYCLES, SQ_LDS_BANK_CONFLICT,
+    SQ_INSTS_LDS, SQ_INSTS_MFMA, GRBM_GUI_ACTIVE): per kernel the fraction of
+    the waves' cycles spent waiting on a memory or LDS counter (SQ_WAIT_ANY /
+    SQ_WAVE_CYCLES) and waiting to issue (SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES,
+    which includes a SIMD's other waves holding the issue slot), and LDS
+    bank-conflict cycles per LDS instruction."""
+    out_path, csv_path = args.stall_summary
+    s = counter_summary([csv_path])
+    res = {}
+    for k, c in s.items():
+        wc = c.get("SQ_WAVE_CYCLES", 0.0)
+        if wc <= 0 or "duration_ns" not in c:
+            continue
+        if not (k.startswith(("ns_", "pack", "adamw", "fp8_", "splitk")) or "butterfly" in k):
+            continue
+        res[k] = {"dispatches": c["dispatches"], "avg_ms": round(c["duration_ns"] * 1e-6, 4),
+                  "wait_any_frac": round(c["SQ_WAIT_ANY"] / wc, 3),
+                  "wait_inst_frac": round(c["SQ_WAIT_INST_ANY"] / wc, 3),
+                  "lds_conflict_cycles_per_lds_inst": round(c["SQ_LDS_BANK_CONFLICT"] / max(1.0, c["SQ_INSTS_LDS"]), 2)}
+    Path(out_path).write_text(json.dumps({"kernels": res}, indent=1) + "\n")
+    print(json.dumps(res, indent=1))
